@@ -1,0 +1,356 @@
+#!/usr/bin/env python
+"""Fused-MoE benchmark on one MI355X.
+
+Headline (``value``): Mixtral-8x7B-shape bf16 fused MoE at M=4096 tokens
+(prefill), whole op per step = alignment + GEMM1+SiLU +
+GEMM2 + top-k sum, inputs (x, weights, top-k routing) resident in HBM.
+Unit TFLOP/s with FLOPs = 6*M*k*K*N.
+
+Also on the same line:
+  roofline      dominant kernel (GEMM1+SiLU) timed with HIP events on the
+                launch stream over its own measured loop;
+  cpu_baseline  the CPU oracle (a restatement of the reference, fp32 torch on
+                the host cores) on a bounded token sample of the same workload;
+  secondary     north-star points: DeepSeek-V3-shape fp8 W8A8 at M=4096
+                (prefill, % fp8 MFMA peak and % of min(peak, AI*BW)) and
+                Mixtral-shape W4A16 decode at M in {1, 16} (% HBM peak).
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "flaggems-sglang_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK = {"bf16": 2500.0, "fp8": 5000.0, "hbm_gbs": 8000.0}  # MI355X dense TFLOP/s, GB/s
+
+WORKLOADS = {
+    # name: (M, K, N, E, k, wtype, routing)
+    "mixtral_bf16_m4096": (4096, 4096, 14336, 8, 2, "bf16", "softmax"),
+    "mixtral_bf16_m1": (1, 4096, 14336, 8, 2, "bf16", "softmax"),
+    "mixtral_bf16_m16": (16, 4096, 14336, 8, 2, "bf16", "softmax"),
+    "qwen3_bf16_m8192": (8192, 2048, 768, 128, 8, "bf16", "softmax_bias"),
+    "dsv3_fp8_m4096": (4096, 7168, 2048, 256, 8, "fp8", "grouped"),
+    "dsv3_fp8_m8192": (8192, 7168, 2048, 256, 8, "fp8", "grouped"),
+    "dsv3_fp8_m1": (1, 7168, 2048, 256, 8, "fp8", "grouped"),
+    "mixtral_w4a16_m1": (1, 4096, 14336, 8, 2, "int4", "softmax"),
+    "mixtral_w4a16_m16": (16, 4096, 14336, 8, 2, "int4", "softmax"),
+}
+
+
+def _gen_weights(E, R, C, gen, dev, wtype, chunk=8):
+    """N(0, 0.02) weights [E, R, C], quantized per wtype; generated a few
+    experts at a time so the bf16 staging copy stays small."""
+    import torch
+
+    from flaggems_sglang import quant as Q
+
+    outs = []
+    for e0 in range(0, E, chunk):
+        e1 = min(E, e0 + chunk)
+        w = (torch.randn(e1 - e0, R, C, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        if wtype == "bf16":
+            outs.append((w,))
+        elif wtype == "fp8":
+            outs.append(Q.quantize_fp8_block(w))
+        else:
+            outs.append(Q.quantize_int4_group(w))
+        del w
+    if wtype == "int4":
+        # scales / zeros are [E, G, R]: concatenate along experts as well
+        return tuple(torch.cat([o[i] for o in outs]) for i in range(3))
+    return tuple(torch.cat([o[i] for o in outs]) for i in range(len(outs[0])))
+
+
+def make_problem(name, seed=0):
+    import torch
+
+    import flaggems_sglang
+
+    M, K, N, E, k, wtype, routing = WORKLOADS[name]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(seed + M + K + N + E + k)
+    x = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+    w13 = _gen_weights(E, 2 * N, K, gen, dev, wtype)
+    w2 = _gen_weights(E, K, N, gen, dev, wtype)
+    logits = torch.randn(M, E, device=dev, generator=gen)
+    if routing == "grouped":
+        tw, ti = flaggems_sglang.grouped_topk(logits, k, 8, 4)
+    else:
+        if routing == "softmax_bias":
+            logits = logits + torch.randn(E, device=dev, generator=gen)[None] * 0.5
+        tw, ti = flaggems_sglang.topk_softmax(logits, k)
+    kw = {}
+    if wtype == "fp8":
+        kw = dict(use_fp8_w8a8=True, w1_scale=w13[1], w2_scale=w2[1], block_shape=[128, 128])
+    elif wtype == "int4":
+        kw = dict(use_int4_w4a16=True, w1_scale=w13[1], w2_scale=w2[1], w1_zp=w13[2], w2_zp=w2[2])
+    return dict(name=name, M=M, K=K, N=N, E=E, k=k, wtype=wtype, x=x, w13=w13[0], w2=w2[0],
+                tw=tw, ti=ti, kw=kw)
+
+
+def flops(p):
+    return 6.0 * p["M"] * p["k"] * p["K"] * p["N"]
+
+
+def weight_bytes_touched(p):
+    """Bytes of the experts the routing actually hits (+ scales / zeros)."""
+    import torch
+
+    hit = torch.bincount(p["ti"].flatten().long(), minlength=p["E"]).gt(0).sum().item()
+    K, N = p["K"], p["N"]
+    if p["wtype"] == "bf16":
+        per = 3 * K * N * 2
+    elif p["wtype"] == "fp8":
+        per = 3 * K * N + 4 * (2 * N // 128) * (K // 128) + 4 * (K // 128) * (N // 128)
+    else:
+        per = 3 * K * N // 2 + 2 * (K // 128) * 2 * N + (K // 128) * N + 2 * (N // 128) * K + (N // 128) * K // 2
+    return hit, hit * per
+
+
+def run_op(p, path=0):
+    import flaggems_sglang
+
+    return flaggems_sglang.fused_experts(p["x"], p["w13"], p["w2"], p["tw"], p["ti"], path=path, **p["kw"])
+
+
+def time_op(p, steps, warmup, path=0):
+    import torch
+
+    for _ in range(warmup):
+        run_op(p, path)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run_op(p, path)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def stage_times(p, reps=10):
+    """Per-stage device time (ms) of one fused call, from HIP events recorded on
+    the launch stream around each C-ABI stage (same kernels as the fused call)."""
+    import torch
+
+    from flaggems_sglang import _lib
+    from flaggems_sglang.ops import fused_moe as F
+
+    L = _lib.lib()
+    M, K, N, E, k = p["M"], p["K"], p["N"], p["E"], p["k"]
+    wt = {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4}[p["wtype"]]
+    bm = L.fmoe_choose_block_m(wt, M, k, E, 0)
+    kw = p["kw"]
+    s13, s2 = kw.get("w1_scale"), kw.get("w2_scale")
+    z13, z2 = kw.get("w1_zp"), kw.get("w2_zp")
+    st = torch.cuda.current_stream().cuda_stream
+    names = ["align", "quant_x", "gemm1", "quant_act", "gemm2", "moe_sum"]
+    acc = {n: 0.0 for n in names}
+    slots = M * k
+    act = torch.empty(slots, N, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(M, K, dtype=torch.bfloat16, device="cuda")
+    for it in range(reps + 2):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        ev[0].record()
+        a = F._align(p["tw"], p["ti"], E, bm, False)
+        r = _lib.Routing(a.topk_indx.data_ptr(), a.gate_indx.data_ptr(), a.gate_scal.data_ptr(),
+                         a.offs_raw.data_ptr(), a.tile_map.data_ptr(), a.n_tiles.data_ptr(), M, k, E,
+                         bm, L.fmoe_max_tiles(slots, E))
+        ev[1].record()
+        xa, xs = p["x"], None
+        if wt == _lib.W_FP8:
+            xa, xs = F.per_token_group_quant_fp8(p["x"])
+        ev[2].record()
+        _lib.check(L.fmoe_gemm1(wt, xa.data_ptr(), _lib.ptr(xs), p["w13"].data_ptr(), _lib.ptr(s13),
+                                _lib.ptr(z13), K, N, ctypes.byref(r), 0, act.data_ptr(), 0, st), "gemm1")
+        ev[3].record()
+        aa, as_ = act, None
+        if wt == _lib.W_FP8:
+            aa, as_ = F.per_token_group_quant_fp8(act)
+        ev[4].record()
+        splits = L.fmoe_gemm2_splits(wt, K, N, ctypes.byref(r), 0)
+        y = torch.empty(splits, slots, K, dtype=torch.float32, device="cuda")
+        _lib.check(L.fmoe_gemm2(wt, aa.data_ptr(), _lib.ptr(as_), p["w2"].data_ptr(), _lib.ptr(s2),
+                                _lib.ptr(z2), K, N, ctypes.byref(r), 1, y.data_ptr(), splits, 0, st), "gemm2")
+        ev[5].record()
+        _lib.check(L.fmoe_moe_sum(y.data_ptr(), splits, a.gate_indx.data_ptr(), M, k, K, 1.0,
+                                  out.data_ptr(), st), "moe_sum")
+        ev[6].record()
+        torch.cuda.synchronize()
+        if it >= 2:
+            for i, n in enumerate(names):
+                acc[n] += ev[i].elapsed_time(ev[i + 1]) / reps
+    acc["block_m"] = bm
+    return acc
+
+
+def cpu_baseline(p, budget_s=10.0):
+    """The CPU oracle (fp32 torch restatement of the reference path) on the
+    first S tokens of the same problem, S sized to about budget_s seconds."""
+    import torch
+
+    from oracle import fused_moe_oracle as O
+
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    used = sorted(set(p["ti"].flatten().tolist()))
+    if p["wtype"] != "bf16":
+        return None
+    w13 = p["w13"].cpu()
+    w2 = p["w2"].cpu()
+    x = p["x"].cpu()
+    tw = p["tw"].cpu()
+    ti = p["ti"].cpu()
+
+    def run(S):
+        t0 = time.perf_counter()
+        O.fused_experts(x[:S], w13, w2, tw[:S], ti[:S])
+        return time.perf_counter() - t0
+
+    S = min(p["M"], 64)
+    t = run(S)
+    if t < budget_s / 2 and S < p["M"]:
+        S = int(min(p["M"], max(S, S * budget_s / max(t, 1e-3))))
+        t = run(S)
+    del used
+    f = 6.0 * S * p["k"] * p["K"] * p["N"]
+    return {"value": round(f / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"first {S} of {p['M']} tokens, oracle/fused_moe_oracle.py fused_experts "
+                      f"(fp32 torch on CPU, includes per-expert weight upcast), {t:.1f} s"}
+
+
+def _load_traffic(name):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def measure(name, steps, warmup):
+    import torch
+
+    p = make_problem(name)
+    t = time_op(p, steps, warmup)
+    stages = stage_times(p)
+    f = flops(p)
+    hit, wbytes = weight_bytes_touched(p)
+    io_bytes = p["M"] * p["K"] * (2 if p["wtype"] != "fp8" else 1) + p["M"] * p["K"] * 2
+    res = dict(p=p, t=t, stages=stages, flops=f, experts_hit=hit, bytes=wbytes + io_bytes)
+    torch.cuda.synchronize()
+    return res
+
+
+def roofline_gemm1(res):
+    """GEMM1+SiLU: algorithmic FLOPs 4*M*k*K*N per launch (bound mfma), or for
+    decode the bytes of the touched w13 weights + x (bound hbm)."""
+    p = res["p"]
+    t = res["stages"]["gemm1"] * 1e-3
+    decode = res["stages"]["block_m"] == 16
+    if decode:
+        hit = res["experts_hit"]
+        K, N = p["K"], p["N"]
+        if p["wtype"] == "int4":
+            wb = 2 * N * K // 2 + 2 * (K // 128) * 2 * N + (K // 128) * N
+        elif p["wtype"] == "fp8":
+            wb = 2 * N * K + 4 * (2 * N // 128) * (K // 128)
+        else:
+            wb = 2 * N * K * 2
+        by = hit * wb + p["M"] * K * 2
+        ach = by / t / 1e9
+        return {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK["hbm_gbs"], "unit": "GB/s",
+                "frac": round(ach / PEAK["hbm_gbs"], 4), "kernel": "gemm_decode_kernel<GEMM1+SiLU>",
+                "algorithmic_bytes": by, "avg_ms": round(res["stages"]["gemm1"], 4)}
+    fl = 4.0 * p["M"] * p["k"] * p["K"] * p["N"]
+    ach = fl / t / 1e12
+    peak = PEAK["fp8" if p["wtype"] == "fp8" else "bf16"]
+    return {"bound": "mfma", "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
+            "frac": round(ach / peak, 4), "kernel": "gemm_prefill_kernel<GEMM1+SiLU>",
+            "algorithmic_flops": fl, "avg_ms": round(res["stages"]["gemm1"], 4)}
+
+
+def secondary_entry(res):
+    p = res["p"]
+    t = res["t"]
+    tf = res["flops"] / t / 1e12
+    gbs = res["bytes"] / t / 1e9
+    e = {"workload": p["name"], "ms": round(t * 1e3, 4), "TFLOP/s": round(tf, 1),
+         "GB/s": round(gbs, 1), "experts_hit": res["experts_hit"],
+         "stages_ms": {k: round(v, 4) for k, v in res["stages"].items() if k != "block_m"},
+         "block_m": res["stages"]["block_m"]}
+    if res["stages"]["block_m"] == 16:
+        e["frac_hbm_peak"] = round(gbs / PEAK["hbm_gbs"], 4)
+    else:
+        peak = PEAK["fp8" if p["wtype"] == "fp8" else "bf16"]
+        ai = res["flops"] / res["bytes"]
+        cap = min(peak, ai * PEAK["hbm_gbs"] / 1e3)
+        e["frac_mfma_peak"] = round(tf / peak, 4)
+        e["frac_of_min_peak_ai_bw"] = round(tf / cap, 4)
+    return e
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="mixtral_bf16_m4096", choices=sorted(WORKLOADS))
+    ap.add_argument("--secondary", default="dsv3_fp8_m4096,mixtral_w4a16_m1,mixtral_w4a16_m16",
+                    help="comma list of extra workloads reported in 'secondary' ('' for none)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the fused-MoE kernels on one "
+              "device's share); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
+
+    head = measure(args.workload, args.steps, args.warmup)
+    p = head["p"]
+    line = {
+        "metric": "fused_moe TFLOP/s & % MFMA peak (prefill); HBM GB/s % peak (decode), 1 GPU",
+        "value": round(head["flops"] / head["t"] / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["t"] * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {"bf16": "bf16", "fp8": "fp8-e4m3 (fp32 acc)", "int4": "int4 w / bf16 a"}[p["wtype"]],
+        "data": "synthetic: x~N(0,1), weights~N(0,0.02) random-init, router logits~N(0,1)",
+        "config": {"workload": p["name"], "M": p["M"], "K": p["K"], "N": p["N"], "E": p["E"],
+                   "top_k": p["k"], "weights": p["wtype"], "global_batch": p["M"],
+                   "parallelism": "single GPU"},
+        "stages_ms": {k: round(v, 4) for k, v in head["stages"].items() if k != "block_m"},
+    }
+    rl = roofline_gemm1(head)
+    rl["traffic"] = _load_traffic(p["name"])
+    line["roofline"] = rl
+    sec = []
+    for name in [s for s in args.secondary.split(",") if s and s != args.workload]:
+        del_keys = None
+        r = measure(name, max(5, args.steps // 2), args.warmup)
+        sec.append(secondary_entry(r))
+        del r, del_keys
+        torch.cuda.empty_cache()
+    line["secondary"] = sec
+    line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(p)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

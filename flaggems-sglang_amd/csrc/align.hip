@@ -1,0 +1,355 @@
+// moe_align: top-k routing -> expert-sorted slot order, ExptData tile map and
+// SGLang's padded sorted_token_ids, bit-exact and deterministic.
+//
+// Replaces _standard_topk_to_triton_kernels (ops/fused_moe.py:103-130) and
+// the compute_expt_data_torch call at :124.  Three phases over chunks of 256
+// tokens (k*256 slots):
+//   rows    per token: order its k ids ascending (rank by counting, ties by
+//           column), write expt_indx / expt_scal, count the chunk's per-expert
+//           histogram in LDS;
+//   scan    one workgroup: per expert, exclusive prefix over chunks, then the
+//           exclusive scan over experts (token_offs_raw), the padded tile
+//           offsets (token_offs_pad) and the tile map;
+//   scatter per chunk, in slot order: a slot's rank among equal experts is
+//           found with wave ballots (no atomics decide a position), so each
+//           expert's slots keep ascending flat order — the stable argsort of
+//           :118 — and every run writes identical bits.
+// For one chunk (M <= 256) the three phases run in a single workgroup launch.
+#include "common.hpp"
+
+namespace fmoe {
+
+constexpr int kAlignThreads = 256;
+constexpr int kMaxExperts = 1024;
+
+struct AlignParams {
+  const int32_t* ids;
+  const float* w;
+  int64_t M;
+  int k;
+  int E;
+  int bm;
+  int64_t max_tiles;
+  int64_t sorted_cap;  // length of sorted_token_ids
+  int n_chunks;
+  int32_t* chunk_hist;  // [n_chunks, E]
+  int32_t* chunk_base;  // [n_chunks, E]
+  int32_t* sort_col;    // [M*k] original column of each row-sorted entry
+  fmoe_align_out o;
+};
+
+// ---- phase 1: per-token sort + chunk histogram
+__device__ void phase_rows(const AlignParams& p, int c, int* h) {
+  const int tid = threadIdx.x;
+  for (int e = tid; e < p.E; e += kAlignThreads) h[e] = 0;
+  __syncthreads();
+  const int64_t t = static_cast<int64_t>(c) * kAlignThreads + tid;
+  if (t < p.M) {
+    const int32_t* row = p.ids + t * p.k;
+    const float* wr = p.w + t * p.k;
+    for (int j = 0; j < p.k; ++j) {
+      int idj = row[j];
+      int rank = 0;
+      for (int i = 0; i < p.k; ++i) {
+        int idi = row[i];
+        rank += (idi < idj) || (idi == idj && i < j);
+      }
+      int64_t f = t * p.k + rank;
+      p.o.expt_indx[f] = idj;
+      p.o.expt_scal[f] = wr[j];
+      p.sort_col[f] = j;
+      if (idj >= 0 && idj < p.E) atomicAdd(&h[idj], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < p.E; e += kAlignThreads) p.chunk_hist[static_cast<int64_t>(c) * p.E + e] = h[e];
+}
+
+// Exclusive scan of one value per thread over the 256-thread block.
+__device__ int block_exclusive_scan(int v, int* lds_tmp, int* total) {
+  const int lane = threadIdx.x % kWave, wid = threadIdx.x / kWave;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  if (lane == kWave - 1) lds_tmp[wid] = x;
+  __syncthreads();
+  int wbase = 0, tot = 0;
+  for (int i = 0; i < kAlignThreads / kWave; ++i) {
+    int s = lds_tmp[i];
+    if (i < wid) wbase += s;
+    tot += s;
+  }
+  __syncthreads();
+  *total = tot;
+  return wbase + x - v;
+}
+
+// ---- phase 2: prefix over chunks and experts, ExptData, SGLang block ids.
+// hist_in != nullptr: histogram given directly (fmoe_expt_data); no chunks.
+__device__ void phase_scan(const AlignParams& p, const int32_t* hist_in, int* offs_pad_lds,
+                           int* tmp) {
+  const int tid = threadIdx.x;
+  constexpr int PER = kMaxExperts / kAlignThreads;  // experts per thread
+  int hv[PER], tv[PER];
+  int hsum = 0, tsum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    int e = tid * PER + i;
+    int run = 0;
+    if (e < p.E) {
+      if (hist_in) {
+        run = hist_in[e];
+      } else {
+        for (int c = 0; c < p.n_chunks; ++c) {
+          int64_t ix = static_cast<int64_t>(c) * p.E + e;
+          int v = p.chunk_hist[ix];
+          p.chunk_base[ix] = run;
+          run += v;
+        }
+      }
+    }
+    hv[i] = run;
+    tv[i] = (run + p.bm - 1) / p.bm;
+    hsum += hv[i];
+    tsum += tv[i];
+  }
+  int htot, ttot;
+  int hbase = block_exclusive_scan(hsum, tmp, &htot);
+  int tbase = block_exclusive_scan(tsum, tmp, &ttot);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    int e = tid * PER + i;
+    if (e < p.E) {
+      if (p.o.hist) p.o.hist[e] = hv[i];
+      p.o.offs_raw[e] = hbase;
+      p.o.offs_pad[e] = tbase;
+      offs_pad_lds[e] = tbase;
+    }
+    hbase += hv[i];
+    tbase += tv[i];
+  }
+  if (tid == 0) {
+    p.o.offs_raw[p.E] = htot;
+    p.o.offs_pad[p.E] = ttot;
+    offs_pad_lds[p.E] = ttot;
+    p.o.n_tiles[0] = ttot;
+    if (p.o.num_tokens_post_padded) p.o.num_tokens_post_padded[0] = ttot * p.bm;
+  }
+  __syncthreads();
+  // tile map: tile tt belongs to the last expert whose padded offset <= tt
+  const int64_t nblk_cap = p.o.expert_ids ? p.sorted_cap / p.bm + 1 : 0;
+  const int64_t lim = p.max_tiles > nblk_cap ? p.max_tiles : nblk_cap;
+  for (int64_t tt = tid; tt < lim; tt += kAlignThreads) {
+    int val = -1, ex = -1;
+    if (tt < ttot) {
+      int lo = 0, hi = p.E;  // offs_pad_lds[lo] <= tt < offs_pad_lds[hi]
+      while (hi - lo > 1) {
+        int mid = (lo + hi) >> 1;
+        if (offs_pad_lds[mid] <= tt) lo = mid; else hi = mid;
+      }
+      ex = lo;
+      val = (static_cast<int>(tt - offs_pad_lds[lo]) << 16) | lo;
+    }
+    if (tt < p.max_tiles) p.o.tile_map[tt] = val;
+    if (tt < nblk_cap) p.o.expert_ids[tt] = ex;
+  }
+}
+
+// ---- phase 3: stable scatter of one chunk
+__device__ void phase_scatter(const AlignParams& p, int c, int* run, int (*wcnt)[kMaxExperts],
+                              int* base, int* padshift) {
+  const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
+  for (int e = tid; e < p.E; e += kAlignThreads) {
+    run[e] = 0;
+    for (int w = 0; w < kAlignThreads / kWave; ++w) wcnt[w][e] = 0;
+    int ob = p.o.offs_raw[e];
+    base[e] = ob + p.chunk_base[static_cast<int64_t>(c) * p.E + e];
+    padshift[e] = p.o.offs_pad[e] * p.bm - ob;
+  }
+  __syncthreads();
+  const int64_t n = p.M * p.k;
+  const int64_t f0 = static_cast<int64_t>(c) * kAlignThreads * p.k;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (int it = 0; it < p.k; ++it) {
+    const int64_t f = f0 + static_cast<int64_t>(it) * kAlignThreads + tid;
+    int e = p.E;  // marker: no expert (past the end, or an out-of-range id)
+    if (f < n) {
+      int v = p.o.expt_indx[f];
+      if (v >= 0 && v < p.E) e = v;
+      else p.o.gate_indx[f] = -1;
+    }
+    // lanes holding the same expert: AND of per-bit ballots (11 bits: E <= 1024)
+    uint64_t m = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 11; ++b) {
+      int bit = (e >> b) & 1;
+      uint64_t v = __ballot(bit);
+      m &= bit ? v : ~v;
+    }
+    const int r = __popcll(m & lt);
+    const int cnt = __popcll(m);
+    const bool live = e < p.E;
+    const bool leader = live && r == cnt - 1;
+    if (leader) wcnt[wid][e] = cnt;
+    __syncthreads();
+    if (live) {
+      int before = run[e];
+      for (int w = 0; w < wid; ++w) before += wcnt[w][e];
+      const int pos = base[e] + before + r;
+      p.o.topk_indx[pos] = static_cast<int32_t>(f);
+      p.o.gate_indx[f] = pos;
+      p.o.gate_scal[pos] = p.o.expt_scal[f];
+      if (p.o.sorted_token_ids) {
+        const int64_t t = f / p.k;
+        p.o.sorted_token_ids[pos + padshift[e]] = static_cast<int32_t>(t * p.k + p.sort_col[f]);
+      }
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&run[e], cnt);  // integer sum: order-independent
+      wcnt[wid][e] = 0;
+    }
+    __syncthreads();
+  }
+}
+
+__device__ void fill_sentinel(const AlignParams& p, int64_t start, int64_t stride) {
+  if (!p.o.sorted_token_ids) return;
+  const int32_t sentinel = static_cast<int32_t>(p.M * p.k);
+  for (int64_t i = start; i < p.sorted_cap; i += stride) p.o.sorted_token_ids[i] = sentinel;
+}
+
+__global__ __launch_bounds__(kAlignThreads) void align_rows_kernel(AlignParams p) {
+  __shared__ int h[kMaxExperts];
+  phase_rows(p, blockIdx.x, h);
+  fill_sentinel(p, static_cast<int64_t>(blockIdx.x) * kAlignThreads + threadIdx.x,
+                static_cast<int64_t>(gridDim.x) * kAlignThreads);
+}
+
+__global__ __launch_bounds__(kAlignThreads) void align_scan_kernel(AlignParams p, const int32_t* hist_in) {
+  __shared__ int offs_pad_lds[kMaxExperts + 1];
+  __shared__ int tmp[kAlignThreads / kWave];
+  phase_scan(p, hist_in, offs_pad_lds, tmp);
+}
+
+__global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(AlignParams p) {
+  __shared__ int run[kMaxExperts];
+  __shared__ int wcnt[kAlignThreads / kWave][kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int padshift[kMaxExperts];
+  phase_scatter(p, blockIdx.x, run, wcnt, base, padshift);
+}
+
+// All three phases in one workgroup (one chunk: M <= 256).
+__global__ __launch_bounds__(kAlignThreads) void align_small_kernel(AlignParams p) {
+  __shared__ int run[kMaxExperts];
+  __shared__ int wcnt[kAlignThreads / kWave][kMaxExperts];
+  __shared__ int base[kMaxExperts];
+  __shared__ int padshift[kMaxExperts + 1];
+  __shared__ int tmp[kAlignThreads / kWave];
+  fill_sentinel(p, threadIdx.x, kAlignThreads);
+  phase_rows(p, 0, run);
+  __syncthreads();
+  phase_scan(p, nullptr, padshift, tmp);
+  __syncthreads();
+  phase_scatter(p, 0, run, wcnt, base, padshift);
+}
+
+}  // namespace fmoe
+
+using namespace fmoe;
+using fmoe_host::check_launch;
+using fmoe_host::fail;
+
+namespace {
+int64_t n_chunks_for(int64_t M) { return (M + kAlignThreads - 1) / kAlignThreads; }
+size_t align_up(size_t v) { return (v + 255) & ~size_t(255); }
+}  // namespace
+
+extern "C" int64_t fmoe_max_tiles(int64_t n_slots, int E) {
+  // triton_kernels.routing length (smallest tile height 16): one tile per
+  // slot while slots <= E, else every non-empty expert may waste a partial tile.
+  if (n_slots <= E) return n_slots > 0 ? n_slots : 1;
+  return E - 1 + (n_slots - E + 1 + 15) / 16;
+}
+
+extern "C" int64_t fmoe_sorted_ids_len(int64_t n_slots, int E, int block_m) {
+  return n_slots + static_cast<int64_t>(E) * (block_m - 1);
+}
+
+extern "C" size_t fmoe_align_workspace_bytes(int64_t M, int k, int E) {
+  const int64_t C = n_chunks_for(M);
+  return 2 * align_up(sizeof(int32_t) * C * E) + align_up(sizeof(int32_t) * M * k);
+}
+
+extern "C" int fmoe_align(const int32_t* topk_ids, const float* topk_weights, int64_t M, int k,
+                          int E, int block_m, const fmoe_align_out* out, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  if (!out) return fail(FMOE_ERR_INVALID, "align: null output struct");
+  if (M < 0 || k < 1 || k > 32 || E < 1 || E > kMaxExperts)
+    return fail(FMOE_ERR_INVALID, "align: need 1 <= k <= 32, 1 <= E <= %d (M=%lld k=%d E=%d)",
+                kMaxExperts, static_cast<long long>(M), k, E);
+  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128)
+    return fail(FMOE_ERR_UNSUPPORTED, "align: block_m=%d is not supported", block_m);
+  if (M * k > (int64_t(1) << 31) - 1 || M * k / block_m + E >= (1 << 15) * 2)
+    return fail(FMOE_ERR_UNSUPPORTED, "align: %lld slots is not supported", static_cast<long long>(M * k));
+  const fmoe_align_out& o = *out;
+  if (!o.expt_indx || !o.expt_scal || !o.topk_indx || !o.gate_indx || !o.gate_scal ||
+      !o.offs_raw || !o.offs_pad || !o.tile_map || !o.n_tiles)
+    return fail(FMOE_ERR_INVALID, "align: a required output pointer is null");
+  if (workspace_bytes < fmoe_align_workspace_bytes(M, k, E))
+    return fail(FMOE_ERR_WORKSPACE, "align: workspace %zu < %zu bytes", workspace_bytes,
+                fmoe_align_workspace_bytes(M, k, E));
+  if (M > 0 && (!topk_ids || !topk_weights)) return fail(FMOE_ERR_INVALID, "align: null input");
+
+  AlignParams p{};
+  p.ids = topk_ids;
+  p.w = topk_weights;
+  p.M = M;
+  p.k = k;
+  p.E = E;
+  p.bm = block_m;
+  p.max_tiles = fmoe_max_tiles(M * k, E);
+  p.sorted_cap = fmoe_sorted_ids_len(M * k, E, block_m);
+  p.n_chunks = static_cast<int>(n_chunks_for(M));
+  const int64_t C = p.n_chunks;
+  char* ws = static_cast<char*>(workspace);
+  p.chunk_hist = reinterpret_cast<int32_t*>(ws);
+  p.chunk_base = reinterpret_cast<int32_t*>(ws + align_up(sizeof(int32_t) * C * E));
+  p.sort_col = reinterpret_cast<int32_t*>(ws + 2 * align_up(sizeof(int32_t) * C * E));
+  p.o = o;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (C <= 1) {
+    if (C == 0) p.n_chunks = 1;  // M == 0: rows phase writes nothing; scan yields zeros
+    align_small_kernel<<<1, kAlignThreads, 0, s>>>(p);
+  } else {
+    align_rows_kernel<<<static_cast<unsigned>(C), kAlignThreads, 0, s>>>(p);
+    align_scan_kernel<<<1, kAlignThreads, 0, s>>>(p, nullptr);
+    align_scatter_kernel<<<static_cast<unsigned>(C), kAlignThreads, 0, s>>>(p);
+  }
+  return check_launch("align");
+}
+
+extern "C" int fmoe_expt_data(const int32_t* hist, int E, int64_t n_slots, int block_m,
+                              int32_t* offs_raw, int32_t* offs_pad, int32_t* tile_map,
+                              int32_t* n_tiles, void* stream) {
+  if (E < 1 || E > kMaxExperts || n_slots < 0)
+    return fail(FMOE_ERR_INVALID, "expt_data: need 1 <= E <= %d", kMaxExperts);
+  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128)
+    return fail(FMOE_ERR_UNSUPPORTED, "expt_data: block_m=%d is not supported", block_m);
+  if (!hist || !offs_raw || !offs_pad || !tile_map || !n_tiles)
+    return fail(FMOE_ERR_INVALID, "expt_data: null pointer");
+  AlignParams p{};
+  p.E = E;
+  p.bm = block_m;
+  p.max_tiles = fmoe_max_tiles(n_slots, E);
+  p.o.offs_raw = offs_raw;
+  p.o.offs_pad = offs_pad;
+  p.o.tile_map = tile_map;
+  p.o.n_tiles = n_tiles;
+  align_scan_kernel<<<1, kAlignThreads, 0, static_cast<hipStream_t>(stream)>>>(p, hist);
+  return check_launch("expt_data");
+}

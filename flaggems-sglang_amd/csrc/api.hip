@@ -1,0 +1,301 @@
+// C-ABI entry points of the GEMM stages and the whole fused path.
+#include "gemm.hpp"
+
+namespace fmoe {
+int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s);
+int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
+}  // namespace fmoe
+
+using namespace fmoe;
+using fmoe_host::fail;
+
+namespace {
+
+constexpr int kDecodeBM = 16;
+constexpr int kDecodeBN = 64;
+constexpr int kDecodeTargetWgs = 1024;
+
+size_t al(size_t v) { return (v + 255) & ~size_t(255); }
+
+bool valid_wtype(int wt) { return wt == FMOE_W_BF16 || wt == FMOE_W_FP8 || wt == FMOE_W_INT4; }
+
+WType to_wt(int wt) {
+  return wt == FMOE_W_FP8 ? WType::kFp8 : (wt == FMOE_W_INT4 ? WType::kInt4 : WType::kBf16);
+}
+
+int check_routing(const fmoe_routing* r, const char* who) {
+  if (!r) return fail(FMOE_ERR_INVALID, "%s: null routing", who);
+  if (!r->topk_indx || !r->gate_scal || !r->offs_raw || !r->tile_map || !r->n_tiles)
+    return fail(FMOE_ERR_INVALID, "%s: routing pointer is null", who);
+  if (r->n_tokens < 0 || r->top_k < 1 || r->n_experts < 1 || r->max_tiles < 0)
+    return fail(FMOE_ERR_INVALID, "%s: bad routing sizes", who);
+  if (r->block_m != 16 && r->block_m != 64 && r->block_m != 128)
+    return fail(FMOE_ERR_UNSUPPORTED, "%s: block_m=%d is not supported", who, r->block_m);
+  return FMOE_OK;
+}
+
+// Decode (block_m 16) or prefill (64 / 128) kernels follow the routing's tile height.
+bool is_decode(const fmoe_routing* r) { return r->block_m == kDecodeBM; }
+
+GemmParams base_params(const fmoe_routing* r) {
+  GemmParams p{};
+  p.topk_indx = r->topk_indx;
+  p.gate_scal = r->gate_scal;
+  p.offs_raw = r->offs_raw;
+  p.tile_map = r->tile_map;
+  p.n_tiles = r->n_tiles;
+  p.top_k = r->top_k;
+  p.max_tiles = r->max_tiles;
+  p.splits = 1;
+  return p;
+}
+
+// Tile height for the fused path: 16 = decode kernels, else the prefill tile.
+int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
+  const int64_t slots = M * k;
+  const int64_t active = slots < E ? slots : E;
+  if (wtype == FMOE_W_INT4 || path == 2) return kDecodeBM;
+  if (path == 1) return slots >= 96 * static_cast<int64_t>(E) ? 128 : 64;
+  if (slots <= kDecodeBM * (active > 0 ? active : 1)) return kDecodeBM;
+  return slots >= 96 * static_cast<int64_t>(E) ? 128 : 64;
+}
+
+}  // namespace
+
+extern "C" int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path) {
+  return choose_block_m(wtype, M, k, E, path);
+}
+
+extern "C" int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_routing* r, int path) {
+  (void)path;
+  if (!r || !is_decode(r)) return 1;
+  const int64_t slots = r->n_tokens * r->top_k;
+  const int64_t est_tiles = slots < r->n_experts ? (slots > 0 ? slots : 1) : r->n_experts;
+  const int64_t ntiles = (K + kDecodeBN - 1) / kDecodeBN;
+  const int64_t wgs = est_tiles * ntiles;
+  const int64_t stage_elems = wtype == FMOE_W_BF16 ? 64 : 128;
+  const int64_t nk = N / stage_elems;
+  int64_t sp = (kDecodeTargetWgs + wgs - 1) / wgs;
+  const int64_t max_sp = nk / 4 > 1 ? nk / 4 : 1;  // keep >= 4 stages per split (one per wave)
+  if (sp > max_sp) sp = max_sp;
+  if (sp > 64) sp = 64;
+  return static_cast<int>(sp < 1 ? 1 : sp);
+}
+
+extern "C" int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const void* w13,
+                          const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
+                          const fmoe_routing* r, int gamma_on_input, void* act, int path,
+                          void* stream) {
+  if (int st = check_routing(r, "gemm1")) return st;
+  if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm1: unknown weight type %d", wtype);
+  if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
+    return fail(FMOE_ERR_UNSUPPORTED, "gemm1: K=%lld N=%lld must be multiples of 128",
+                static_cast<long long>(K), static_cast<long long>(N));
+  if (!x || !w13 || !act) return fail(FMOE_ERR_INVALID, "gemm1: null pointer");
+  if (wtype == FMOE_W_FP8 && (!x_scale || !w13_scale))
+    return fail(FMOE_ERR_INVALID, "gemm1: fp8 needs x_scale and w13_scale");
+  if (wtype == FMOE_W_INT4 && (!w13_scale || !w13_zero))
+    return fail(FMOE_ERR_INVALID, "gemm1: int4 needs w13_scale and w13_zero");
+  if (wtype == FMOE_W_INT4 && !is_decode(r))
+    return fail(FMOE_ERR_UNSUPPORTED, "gemm1: int4 weights need block_m=16 routing");
+  if ((path == 1 && is_decode(r)) || (path == 2 && !is_decode(r)))
+    return fail(FMOE_ERR_INVALID, "gemm1: path %d does not match block_m=%d", path, r->block_m);
+  GemmParams p = base_params(r);
+  p.A = static_cast<const uint8_t*>(x);
+  p.a_scale = x_scale;
+  p.B = static_cast<const uint8_t*>(w13);
+  p.b_scale = static_cast<const float*>(w13_scale);
+  p.b_gscale = static_cast<const uint16_t*>(w13_scale);
+  p.b_zero = static_cast<const uint8_t*>(w13_zero);
+  p.Kred = K;
+  p.Nout = 2 * N;
+  p.N_act = N;
+  p.gamma = gamma_on_input;
+  p.out = act;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (is_decode(r)) return launch_decode(to_wt(wtype), Mode::kGemm1Silu, p, s);
+  return launch_prefill(to_wt(wtype), Mode::kGemm1Silu, r->block_m, p, s);
+}
+
+extern "C" int fmoe_gemm2(int wtype, const void* act, const float* act_scale, const void* w2,
+                          const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
+                          const fmoe_routing* r, int apply_gamma, float* y, int splits, int path,
+                          void* stream) {
+  if (int st = check_routing(r, "gemm2")) return st;
+  if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm2: unknown weight type %d", wtype);
+  if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
+    return fail(FMOE_ERR_UNSUPPORTED, "gemm2: K=%lld N=%lld must be multiples of 128",
+                static_cast<long long>(K), static_cast<long long>(N));
+  if (!act || !w2 || !y) return fail(FMOE_ERR_INVALID, "gemm2: null pointer");
+  if (wtype == FMOE_W_FP8 && (!act_scale || !w2_scale))
+    return fail(FMOE_ERR_INVALID, "gemm2: fp8 needs act_scale and w2_scale");
+  if (wtype == FMOE_W_INT4 && (!w2_scale || !w2_zero))
+    return fail(FMOE_ERR_INVALID, "gemm2: int4 needs w2_scale and w2_zero");
+  if (wtype == FMOE_W_INT4 && !is_decode(r))
+    return fail(FMOE_ERR_UNSUPPORTED, "gemm2: int4 weights need block_m=16 routing");
+  if ((path == 1 && is_decode(r)) || (path == 2 && !is_decode(r)))
+    return fail(FMOE_ERR_INVALID, "gemm2: path %d does not match block_m=%d", path, r->block_m);
+  if (splits < 1 || (splits > 1 && !is_decode(r)))
+    return fail(FMOE_ERR_INVALID, "gemm2: splits=%d (split-K only on the decode path)", splits);
+  GemmParams p = base_params(r);
+  p.A = static_cast<const uint8_t*>(act);
+  p.a_scale = act_scale;
+  p.B = static_cast<const uint8_t*>(w2);
+  p.b_scale = static_cast<const float*>(w2_scale);
+  p.b_gscale = static_cast<const uint16_t*>(w2_scale);
+  p.b_zero = static_cast<const uint8_t*>(w2_zero);
+  p.Kred = N;
+  p.Nout = K;
+  p.N_act = N;
+  p.gamma = apply_gamma;
+  p.out = y;
+  p.splits = splits;
+  p.out_split_stride = r->n_tokens * r->top_k * K;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (is_decode(r)) return launch_decode(to_wt(wtype), Mode::kGemm2, p, s);
+  return launch_prefill(to_wt(wtype), Mode::kGemm2, r->block_m, p, s);
+}
+
+// ------------------------------------------------------------ fused path
+namespace {
+
+struct FusedLayout {
+  int bm;
+  int splits;
+  int64_t max_tiles;
+  size_t align_ws, expt_indx, expt_scal, topk_indx, gate_indx, gate_scal, hist, offs_raw,
+      offs_pad, tile_map, n_tiles, xq, xs, act, actq, acts, y, total;
+};
+
+int check_fused(const fmoe_fused_args* a) {
+  if (!a) return fail(FMOE_ERR_INVALID, "fused_experts: null args");
+  if (!valid_wtype(a->wtype)) return fail(FMOE_ERR_INVALID, "fused_experts: unknown weight type");
+  if (a->M < 0 || a->E < 1 || a->E > 1024 || a->top_k < 1 || a->top_k > 32 || a->top_k > a->E)
+    return fail(FMOE_ERR_INVALID, "fused_experts: bad M/E/top_k");
+  if (a->K <= 0 || a->N <= 0 || a->K % 128 != 0 || a->N % 128 != 0)
+    return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: K=%lld N=%lld must be multiples of 128",
+                static_cast<long long>(a->K), static_cast<long long>(a->N));
+  if (a->wtype == FMOE_W_INT4 && a->group_size != 128)
+    return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: int4 group_size=%d is not supported",
+                a->group_size);
+  if (a->path < 0 || a->path > 2) return fail(FMOE_ERR_INVALID, "fused_experts: path %d", a->path);
+  if (a->M > 65535) return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: M > 65535 is not supported");
+  return FMOE_OK;
+}
+
+FusedLayout layout(const fmoe_fused_args* a) {
+  FusedLayout L{};
+  const int64_t slots = a->M * a->top_k;
+  L.bm = choose_block_m(a->wtype, a->M, a->top_k, a->E, a->path);
+  L.max_tiles = fmoe_max_tiles(slots, a->E);
+  fmoe_routing r{};
+  r.n_tokens = a->M;
+  r.top_k = a->top_k;
+  r.n_experts = a->E;
+  r.block_m = L.bm;
+  L.splits = fmoe_gemm2_splits(a->wtype, a->K, a->N, &r, 0);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += al(bytes);
+    return o;
+  };
+  L.align_ws = take(fmoe_align_workspace_bytes(a->M, a->top_k, a->E));
+  L.expt_indx = take(4 * slots);
+  L.expt_scal = take(4 * slots);
+  L.topk_indx = take(4 * slots);
+  L.gate_indx = take(4 * slots);
+  L.gate_scal = take(4 * slots);
+  L.hist = take(4 * a->E);
+  L.offs_raw = take(4 * (a->E + 1));
+  L.offs_pad = take(4 * (a->E + 1));
+  L.tile_map = take(4 * L.max_tiles);
+  L.n_tiles = take(4);
+  const bool fp8 = a->wtype == FMOE_W_FP8;
+  L.xq = take(fp8 ? a->M * a->K : 0);
+  L.xs = take(fp8 ? 4 * a->M * (a->K / 128) : 0);
+  L.act = take(2 * slots * a->N);
+  L.actq = take(fp8 ? slots * a->N : 0);
+  L.acts = take(fp8 ? 4 * slots * (a->N / 128) : 0);
+  L.y = take(4 * static_cast<size_t>(L.splits) * slots * a->K);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a) {
+  if (check_fused(a) != FMOE_OK) return 0;
+  return layout(a).total;
+}
+
+extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
+  if (int st = check_fused(a)) return st;
+  if (a->M == 0) return FMOE_OK;
+  if (!a->x || !a->w13 || !a->w2 || !a->topk_ids || !a->topk_weights || !a->out)
+    return fail(FMOE_ERR_INVALID, "fused_experts: null pointer");
+  const FusedLayout L = layout(a);
+  if (!a->workspace || a->workspace_bytes < L.total)
+    return fail(FMOE_ERR_WORKSPACE, "fused_experts: workspace %zu < %zu bytes", a->workspace_bytes,
+                L.total);
+  char* ws = static_cast<char*>(a->workspace);
+  auto at = [&](size_t o) { return static_cast<void*>(ws + o); };
+  const int64_t slots = a->M * a->top_k;
+
+  fmoe_align_out o{};
+  o.expt_indx = static_cast<int32_t*>(at(L.expt_indx));
+  o.expt_scal = static_cast<float*>(at(L.expt_scal));
+  o.topk_indx = static_cast<int32_t*>(at(L.topk_indx));
+  o.gate_indx = static_cast<int32_t*>(at(L.gate_indx));
+  o.gate_scal = static_cast<float*>(at(L.gate_scal));
+  o.hist = static_cast<int32_t*>(at(L.hist));
+  o.offs_raw = static_cast<int32_t*>(at(L.offs_raw));
+  o.offs_pad = static_cast<int32_t*>(at(L.offs_pad));
+  o.tile_map = static_cast<int32_t*>(at(L.tile_map));
+  o.n_tiles = static_cast<int32_t*>(at(L.n_tiles));
+  if (int st = fmoe_align(a->topk_ids, a->topk_weights, a->M, a->top_k, a->E, L.bm, &o,
+                          at(L.align_ws), fmoe_align_workspace_bytes(a->M, a->top_k, a->E), stream))
+    return st;
+
+  fmoe_routing r{};
+  r.topk_indx = o.topk_indx;
+  r.gate_indx = o.gate_indx;
+  r.gate_scal = o.gate_scal;
+  r.offs_raw = o.offs_raw;
+  r.tile_map = o.tile_map;
+  r.n_tiles = o.n_tiles;
+  r.n_tokens = a->M;
+  r.top_k = a->top_k;
+  r.n_experts = a->E;
+  r.block_m = L.bm;
+  r.max_tiles = static_cast<int32_t>(L.max_tiles);
+
+  const bool fp8 = a->wtype == FMOE_W_FP8;
+  const void* x = a->x;
+  const float* xs = nullptr;
+  if (fp8) {
+    if (int st = fmoe_quant_fp8_group(a->x, a->M, a->K, 128, at(L.xq),
+                                      static_cast<float*>(at(L.xs)), stream))
+      return st;
+    x = at(L.xq);
+    xs = static_cast<const float*>(at(L.xs));
+  }
+  if (int st = fmoe_gemm1(a->wtype, x, xs, a->w13, a->w13_scale, a->w13_zero, a->K, a->N, &r,
+                          a->apply_router_weight_on_input, at(L.act), 0, stream))
+    return st;
+  const void* act = at(L.act);
+  const float* acts = nullptr;
+  if (fp8) {
+    if (int st = fmoe_quant_fp8_group(at(L.act), slots, a->N, 128, at(L.actq),
+                                      static_cast<float*>(at(L.acts)), stream))
+      return st;
+    act = at(L.actq);
+    acts = static_cast<const float*>(at(L.acts));
+  }
+  if (int st = fmoe_gemm2(a->wtype, act, acts, a->w2, a->w2_scale, a->w2_zero, a->K, a->N, &r,
+                          !a->apply_router_weight_on_input, static_cast<float*>(at(L.y)), L.splits,
+                          0, stream))
+    return st;
+  return fmoe_moe_sum(static_cast<const float*>(at(L.y)), L.splits, o.gate_indx, a->M, a->top_k,
+                      a->K, a->routed_scaling_factor, a->out, stream);
+}

@@ -1,0 +1,89 @@
+// Shared device helpers for the gfx950 fused-MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fmoe.h"
+
+namespace fmoe {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
+constexpr float kFp8Max = 448.0f;
+constexpr float kFp8Eps = 1e-10f;
+
+// ---------------------------------------------------------------- numerics
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16, round to nearest even (NaN kept quiet), as torch's .to(bfloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// fp32 -> float8_e4m3fn, round to nearest even.  |f| must already be clamped
+// to <= 448 (callers clamp), so no saturation / NaN path is needed.
+// Normals: keep 3 mantissa bits of the fp32 pattern with RNE, rebias the
+// exponent from 127 to 7.  Below 2^-6 (subnormal): the value in units of
+// 2^-9, rounded to nearest even, is the code itself.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  float a = fabsf(f);
+  uint32_t code;
+  if (a < 0.015625f) {
+    code = static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
+  } else {
+    uint32_t au = __float_as_uint(a);
+    uint32_t t = (au + 0x7ffffu + ((au >> 20) & 1u)) >> 20;
+    code = t - (120u << 3);
+  }
+  return sign | code;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  // ops/fused_moe.py:46 — gate / (1 + exp(-gate)) * up, in fp32
+  return (g / (1.0f + __expf(-g))) * u;
+}
+
+// ------------------------------------------------------------- wave utils
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// XCD-aware remap of a linear workgroup id over `count` live workgroups:
+// hardware hands consecutive ids to different XCDs; this makes each XCD's
+// share a contiguous range of logical tiles so neighbouring tiles (same
+// expert, same weight panel) meet in one XCD's L2.
+__device__ __forceinline__ int xcd_remap(int b, int count) {
+  int x = b % kNumXcd, i = b / kNumXcd;
+  int q = count / kNumXcd, r = count % kNumXcd;
+  return x * q + (x < r ? x : r) + i;
+}
+
+}  // namespace fmoe
+
+// Host-side error reporting shared by the entry points.
+namespace fmoe_host {
+int fail(int status, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace fmoe_host

@@ -1,0 +1,279 @@
+// Decode grouped GEMM: weights streamed straight from HBM into MFMA registers.
+//
+// For small token counts every expert tile holds <= 16 slots, so the work is
+// bound by reading each touched expert's weights once.  A workgroup (4
+// waves) owns 16 slots x 64 weight rows and splits the reduction dim between
+// its waves by interleaved 128-byte stages (wave w takes stages w, w+4, ...),
+// so at any moment the four waves read adjacent 128-byte pieces of the same
+// 64 rows; lane group g = lane/16 reads bytes 32g..32g+31 (int4: 16g..16g+15)
+// of row lane%16 of each 16-row block.  No LDS staging; the per-wave partial
+// accumulators are summed through LDS once at the end.  GEMM2 may further
+// split the reduction across workgroups (`splits`); the partials land in
+// separate y planes that fmoe_moe_sum adds in fixed order.
+//
+// Weight formats:
+//   bf16: 16 elements per lane per stage -> two v_mfma_f32_16x16x32_bf16.
+//   fp8 : 32 elements per lane per stage -> one v_mfma_f32_16x16x128_f8f6f4,
+//         scaled by a_scale * w_scale per 128-wide block.
+//   int4: 32 nibbles per lane per stage (one 128-wide quant group per stage).
+//         A nibble q becomes the bf16 number 128 + q by OR-ing 0x4300 into
+//         its 16-bit lane (exact: bf16 spacing at 128 is 1), so the MFMA
+//         computes sum((128 + q) x); with xs = sum(x) over the group (an MFMA
+//         against a ones vector) the dequantized product is
+//         scale * (sum((128+q) x) - (128 + zero) * xs).
+//         The nibble pairs come out as k = (j, j+4) of each 8-nibble dword;
+//         the activations are permuted the same way with v_perm_b32.
+#include "gemm.hpp"
+
+namespace fmoe {
+namespace decode {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int BM = 16;
+constexpr int BN = 64;
+constexpr int NI = BN / 16;
+
+__device__ __forceinline__ i32x8_t gload32(const uint8_t* p) {
+  i32x4_t lo = *reinterpret_cast<const i32x4_t*>(p);
+  i32x4_t hi = *reinterpret_cast<const i32x4_t*>(p + 16);
+  return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(int a, int b, int c, int d) {
+  return __builtin_bit_cast(bf16x8_t, i32x4_t{a, b, c, d});
+}
+
+template <WType WT, Mode MODE>
+__global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
+  __shared__ f32x4_t red[kWaves][NI][kWave];
+  const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
+  const int mt = blockIdx.x;
+  if (mt >= *p.n_tiles) return;
+  const int nt = blockIdx.y;
+  const int split = blockIdx.z;
+
+  const int tm = p.tile_map[mt];
+  const int e = tm & 0xffff, blk = tm >> 16;
+  const int row_beg = p.offs_raw[e] + blk * BM;
+  const int row_end = min(p.offs_raw[e + 1], row_beg + BM);
+
+  // A rows: row lane%16 of the tile
+  int s_a = row_beg + (lane & 15);
+  if (s_a >= row_end) s_a = row_beg;
+  const int64_t a_row = MODE == Mode::kGemm1Silu ? p.topk_indx[s_a] / p.top_k : s_a;
+  constexpr bool kFp8 = WT == WType::kFp8;
+  constexpr bool kInt4 = WT == WType::kInt4;
+  const int64_t a_bytes = kFp8 ? p.Kred : p.Kred * 2;
+  const uint8_t* a_ptr = p.A + a_row * a_bytes;
+  // stage geometry: bytes of one weight row per stage and reduction elements
+  constexpr int kWStage = kInt4 ? 64 : 128;
+  const int64_t w_bytes = kInt4 ? p.Kred / 2 : (kFp8 ? p.Kred : p.Kred * 2);
+  const int nk = static_cast<int>(w_bytes / kWStage);
+  constexpr int kElems = kInt4 ? 128 : (kFp8 ? 128 : 64);  // reduction elements per stage
+
+  // weight rows of the 4 blocks for this lane
+  const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * w_bytes;
+  int64_t wrow[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    int64_t r;
+    if (MODE == Mode::kGemm1Silu) {
+      int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + (lane & 15);
+      r = j < NI / 2 ? jj : p.N_act + jj;
+    } else {
+      r = static_cast<int64_t>(nt) * BN + j * 16 + (lane & 15);
+      if (r >= p.Nout) r = p.Nout - 1;
+    }
+    wrow[j] = r;
+  }
+  const uint8_t* w_ptr[NI];
+  const int lane_off_w = (lane >> 4) * (kInt4 ? 16 : 32);
+#pragma unroll
+  for (int j = 0; j < NI; ++j) w_ptr[j] = Be + wrow[j] * w_bytes + lane_off_w;
+  const int lane_off_a = (lane >> 4) * (kInt4 ? 64 : 32);
+
+  // fp8 scales
+  const int ksb = static_cast<int>(p.Kred / 128);
+  const float* sa_ptr[4] = {nullptr, nullptr, nullptr, nullptr};
+  const float* sb_ptr[NI] = {};
+  if (kFp8) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int s = row_beg + (lane >> 4) * 4 + r;
+      if (s >= row_end) s = row_beg;
+      int64_t src = MODE == Mode::kGemm1Silu ? p.topk_indx[s] / p.top_k : s;
+      sa_ptr[r] = p.a_scale + src * ksb;
+    }
+    const float* se = p.b_scale + static_cast<int64_t>(e) * (p.Nout / 128) * ksb;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      // block of the block's first row (16-row blocks never straddle 128)
+      int64_t r0 = wrow[j] - (lane & 15);
+      sb_ptr[j] = se + (r0 / 128) * ksb;
+    }
+  }
+
+  f32x4_t acc[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // split-K range over stages
+  const int per_split = (nk + p.splits - 1) / p.splits;
+  const int k_beg = split * per_split;
+  const int k_end = min(nk, k_beg + per_split);
+
+  for (int kt = k_beg + wid; kt < k_end; kt += kWaves) {
+    const int64_t woff = static_cast<int64_t>(kt) * kWStage;
+    const int64_t aoff = static_cast<int64_t>(kt) * kElems * (kFp8 ? 1 : 2);
+    if constexpr (WT == WType::kBf16) {
+      i32x8_t a = gload32(a_ptr + aoff + lane_off_a);
+      i32x8_t b[NI];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) b[j] = gload32(w_ptr[j] + woff);
+      bf16x8_t a0 = as_bf16x8(a[0], a[1], a[2], a[3]), a1 = as_bf16x8(a[4], a[5], a[6], a[7]);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            a0, as_bf16x8(b[j][0], b[j][1], b[j][2], b[j][3]), acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            a1, as_bf16x8(b[j][4], b[j][5], b[j][6], b[j][7]), acc[j], 0, 0, 0);
+      }
+    } else if constexpr (WT == WType::kFp8) {
+      i32x8_t a = gload32(a_ptr + aoff + lane_off_a);
+      i32x8_t b[NI];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) b[j] = gload32(w_ptr[j] + woff);
+      float sa[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sa[r] = sa_ptr[r][kt];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+        t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[j], t, 0, 0, 0, 0, 0, 0);
+        const float sb = sb_ptr[j][kt];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] += t[r] * (sa[r] * sb);
+      }
+    } else {  // int4
+      // activations for this lane: 32 bf16 = elements 32g .. 32g+31 of the stage
+      const uint8_t* ap = a_ptr + aoff + lane_off_a;
+      i32x4_t x4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) x4[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+      i32x4_t w4[NI];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) w4[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+      f32x4_t t[NI], xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NI; ++j) t[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
+      // 8 consecutive elements of group d occupy dwords 4d..4d+3 of x (x4[d])
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int x01 = x4[d][0], x23 = x4[d][1], x45 = x4[d][2], x67 = x4[d][3];
+        const int p04 = __builtin_amdgcn_perm(x45, x01, 0x05040100);
+        const int p15 = __builtin_amdgcn_perm(x45, x01, 0x07060302);
+        const int p26 = __builtin_amdgcn_perm(x67, x23, 0x05040100);
+        const int p37 = __builtin_amdgcn_perm(x67, x23, 0x07060302);
+        const bf16x8_t a = as_bf16x8(p04, p15, p26, p37);
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const unsigned wv = static_cast<unsigned>(w4[j][d]);
+          const int b0 = static_cast<int>((wv & 0x000f000fu) | 0x43004300u);
+          const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
+          const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
+          const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
+          t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b0, b1, b2, b3), t[j], 0, 0, 0);
+        }
+      }
+      // fold zero and scale of group kt for this lane's column
+      const int64_t G = p.Kred / 128;
+      const int64_t gbase = (static_cast<int64_t>(e) * G + kt) * p.Nout;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int64_t col = wrow[j];
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, p.b_gscale[gbase + col]));
+        const uint8_t zb = p.b_zero[(gbase >> 1) + (col >> 1)];
+        const float z = static_cast<float>((col & 1) ? (zb >> 4) : (zb & 15));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[j][r] - (128.0f + z) * xs[r]);
+      }
+    }
+  }
+
+  // ---- reduce the 4 waves' partials
+#pragma unroll
+  for (int j = 0; j < NI; ++j) red[wid][j][lane] = acc[j];
+  __syncthreads();
+  if (wid != 0) return;
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    f32x4_t v = red[0][j][lane];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      f32x4_t u = red[w][j][lane];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] += u[r];
+    }
+    acc[j] = v;
+  }
+
+  const int col16 = lane & 15;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int s = row_beg + (lane >> 4) * 4 + r;
+    if (s >= row_end) continue;
+    const float g = p.gamma ? p.gate_scal[s] : 1.0f;
+    if (MODE == Mode::kGemm1Silu) {
+      uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.N_act;
+#pragma unroll
+      for (int j = 0; j < NI / 2; ++j) {
+        const float gv = round_bf16(acc[j][r] * g);
+        const float uv = round_bf16(acc[j + NI / 2][r] * g);
+        const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + j * 16 + col16;
+        act[col] = f32_to_bf16(silu_mul(gv, uv));
+      }
+    } else {
+      float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
+                 static_cast<int64_t>(s) * p.Nout;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int64_t col = static_cast<int64_t>(nt) * BN + j * 16 + col16;
+        if (col < p.Nout) y[col] = acc[j][r] * g;
+      }
+    }
+  }
+}
+
+}  // namespace decode
+
+int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
+  GemmParams p = p0;
+  const int64_t ncols = mode == Mode::kGemm1Silu ? p.N_act : p.Nout;
+  const int per_tile = mode == Mode::kGemm1Silu ? decode::BN / 2 : decode::BN;
+  p.n_ntiles = static_cast<int>((ncols + per_tile - 1) / per_tile);
+  if (p.max_tiles <= 0) return FMOE_OK;
+  dim3 g(static_cast<unsigned>(p.max_tiles), static_cast<unsigned>(p.n_ntiles),
+         static_cast<unsigned>(mode == Mode::kGemm2 ? p.splits : 1));
+  dim3 b(decode::kThreads);
+#define LAUNCH(WT_, MODE_) decode::gemm_decode_kernel<WT_, MODE_><<<g, b, 0, s>>>(p)
+  if (mode == Mode::kGemm1Silu) {
+    switch (wt) {
+      case WType::kBf16: LAUNCH(WType::kBf16, Mode::kGemm1Silu); break;
+      case WType::kFp8: LAUNCH(WType::kFp8, Mode::kGemm1Silu); break;
+      case WType::kInt4: LAUNCH(WType::kInt4, Mode::kGemm1Silu); break;
+    }
+  } else {
+    switch (wt) {
+      case WType::kBf16: LAUNCH(WType::kBf16, Mode::kGemm2); break;
+      case WType::kFp8: LAUNCH(WType::kFp8, Mode::kGemm2); break;
+      case WType::kInt4: LAUNCH(WType::kInt4, Mode::kGemm2); break;
+    }
+  }
+#undef LAUNCH
+  return fmoe_host::check_launch("gemm_decode");
+}
+
+}  // namespace fmoe

@@ -1,0 +1,112 @@
+// Bandwidth-bound helpers of the fused path:
+//   * dynamic per-token-group fp8 (e4m3fn) quantization of bf16 rows;
+//   * the deterministic top-k combine (moe_sum).
+#include "common.hpp"
+
+namespace fmoe {
+
+// One thread = 8 consecutive bf16 (one 16-byte load); `group / 8` threads
+// cooperate on a group and reduce its amax with xor-shuffles.
+template <int GROUP>
+__global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __restrict__ x,
+                                                              int64_t n_vec, int64_t K,
+                                                              uint8_t* __restrict__ q,
+                                                              float* __restrict__ scale) {
+  constexpr int TPG = GROUP / 8;  // threads per group
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool live = v < n_vec;
+  const int64_t vv = live ? v : 0;
+  i32x4_t raw = *reinterpret_cast<const i32x4_t*>(x + vv * 8);
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w = static_cast<uint32_t>(raw[i]);
+    f[2 * i] = __uint_as_float(w << 16);
+    f[2 * i + 1] = __uint_as_float(w & 0xffff0000u);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(f[i]));
+#pragma unroll
+  for (int o = TPG / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
+  const float s = fmaxf(amax, kFp8Eps) / kFp8Max;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float t = fminf(fmaxf(f[i] / s, -kFp8Max), kFp8Max);
+    uint32_t c = f32_to_e4m3(t);
+    if (i < 4) lo |= c << (8 * i); else hi |= c << (8 * (i - 4));
+  }
+  if (!live) return;
+  *reinterpret_cast<uint2*>(q + vv * 8) = make_uint2(lo, hi);
+  if ((threadIdx.x % TPG) == 0) {
+    const int64_t row = (vv * 8) / K, col = (vv * 8) % K;
+    scale[row * (K / GROUP) + col / GROUP] = s;
+  }
+}
+
+// out[t, c] = bf16(scale * sum_j sum_p y[p][gate_indx[t*k+j], c]); j then p
+// in ascending order.  One thread = 4 columns (16-byte loads).
+__global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ y, int splits,
+                                                      int64_t split_stride,
+                                                      const int32_t* __restrict__ gate_indx,
+                                                      int k, int64_t K, float scale,
+                                                      uint16_t* __restrict__ out) {
+  const int64_t t = blockIdx.y;
+  const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (c >= K) return;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const int s = gate_indx[t * k + j];
+    if (s < 0) continue;  // slot routed to no expert
+    for (int p = 0; p < splits; ++p) {
+      const float4 v = *reinterpret_cast<const float4*>(y + p * split_stride + static_cast<int64_t>(s) * K + c);
+      a0 += v.x;
+      a1 += v.y;
+      a2 += v.z;
+      a3 += v.w;
+    }
+  }
+  const uint32_t w0 = f32_to_bf16(a0 * scale) | (static_cast<uint32_t>(f32_to_bf16(a1 * scale)) << 16);
+  const uint32_t w1 = f32_to_bf16(a2 * scale) | (static_cast<uint32_t>(f32_to_bf16(a3 * scale)) << 16);
+  *reinterpret_cast<uint2*>(out + t * K + c) = make_uint2(w0, w1);
+}
+
+}  // namespace fmoe
+
+using namespace fmoe;
+using fmoe_host::check_launch;
+using fmoe_host::fail;
+
+extern "C" int fmoe_quant_fp8_group(const void* x, int64_t M, int64_t K, int group, void* q,
+                                    float* scale, void* stream) {
+  if (M < 0 || K <= 0 || (group != 64 && group != 128) || K % group != 0)
+    return fail(FMOE_ERR_INVALID, "quant_fp8_group: need K %% group == 0, group in {64,128} (K=%lld group=%d)",
+                static_cast<long long>(K), group);
+  if (M == 0) return FMOE_OK;
+  if (!x || !q || !scale) return fail(FMOE_ERR_INVALID, "quant_fp8_group: null pointer");
+  const int64_t n_vec = M * K / 8;
+  dim3 g(static_cast<unsigned>((n_vec + 255) / 256)), b(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (group == 128)
+    quant_fp8_group_kernel<128><<<g, b, 0, s>>>(static_cast<const uint16_t*>(x), n_vec, K,
+                                                static_cast<uint8_t*>(q), scale);
+  else
+    quant_fp8_group_kernel<64><<<g, b, 0, s>>>(static_cast<const uint16_t*>(x), n_vec, K,
+                                               static_cast<uint8_t*>(q), scale);
+  return check_launch("quant_fp8_group");
+}
+
+extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx, int64_t M, int k,
+                            int64_t K, float scale, void* out, void* stream) {
+  if (M < 0 || k < 1 || K <= 0 || K % 4 != 0 || splits < 1)
+    return fail(FMOE_ERR_INVALID, "moe_sum: need K %% 4 == 0, k >= 1, splits >= 1");
+  if (M == 0) return FMOE_OK;
+  if (M > 65535) return fail(FMOE_ERR_UNSUPPORTED, "moe_sum: M=%lld > 65535 is not supported",
+                             static_cast<long long>(M));
+  if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
+  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
+  moe_sum_kernel<<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
+      y, splits, M * k * K, gate_indx, k, K, scale, static_cast<uint16_t*>(out));
+  return check_launch("moe_sum");
+}

@@ -1,0 +1,542 @@
+"""Fused MoE for MI355X: the host side of FlagGems-sglang's fused-MoE path.
+
+Mirrors ``flaggems_sglang.ops.fused_moe`` of the reference
+(``src/flaggems_sglang/ops/fused_moe.py``): the same entry points
+(``triton_kernel_fused_experts``, ``fused_moe_flagos``), argument meaning and
+error behaviour (``AssertionError("<name> is not supported")``,
+``ValueError`` for an unknown activation).  Every op calls the HIP library
+``libfmoe.so`` through its C ABI (``include/fmoe.h``); nothing here computes
+the MoE in torch.
+
+Additions the reference does not have (its fp8 arguments are asserted off,
+``ops/fused_moe.py:154-169``, and it has no int4 path): the SGLang-style
+plain-tensor ``fused_experts`` with fp8 block-scale W8A8 and int4 W4A16
+weights, the routers ``topk_softmax`` / ``grouped_topk`` and SGLang's
+``moe_align_block_size``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import logging
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from .._lib import W_BF16, W_FP8, W_INT4, check, lib, ptr, require_cuda, stream_of
+
+logger = logging.getLogger(__name__)
+
+_UNSUPPORTED_FEATURE_MSG = "{name} is not supported"
+
+
+# ---------------------------------------------------------------------------
+# routing containers (field names of triton_kernels.routing, which the
+# reference builds at ops/fused_moe.py:125-130)
+# ---------------------------------------------------------------------------
+@dataclass
+class ExptData:
+    hist: torch.Tensor
+    token_offs_raw: torch.Tensor
+    token_offs_pad: dict = field(default_factory=dict)   # block_m -> [E+1] (tiles)
+    block_pid_map: dict = field(default_factory=dict)    # block_m -> [max_tiles]
+    n_tiles: dict = field(default_factory=dict)          # block_m -> [1] device int32
+
+
+@dataclass
+class RoutingData:
+    gate_scal: torch.Tensor
+    expt_hist: torch.Tensor
+    n_expts_tot: int
+    n_expts_act: int
+    expt_data: Optional[ExptData] = None
+
+
+@dataclass
+class GatherIndx:
+    src_indx: torch.Tensor
+    dst_indx: torch.Tensor
+
+
+@dataclass
+class ScatterIndx:
+    src_indx: torch.Tensor
+    dst_indx: torch.Tensor
+
+
+@dataclass
+class CombineInput:
+    """Stand-in for SGLang's StandardCombineInput when SGLang is absent."""
+    hidden_states: torch.Tensor
+
+
+# ---------------------------------------------------------------------------
+# routers
+# ---------------------------------------------------------------------------
+def topk_softmax(gating_output: torch.Tensor, topk: int, renormalize: bool = True):
+    """softmax -> top-k -> renormalise (tests/test_fused_moe.py:24-27).
+
+    Returns ``(topk_weights fp32 [M, k], topk_ids int32 [M, k])``, descending."""
+    require_cuda(gating_output)
+    x = gating_output.float().contiguous()
+    M, E = x.shape
+    w = torch.empty(M, topk, dtype=torch.float32, device=x.device)
+    ids = torch.empty(M, topk, dtype=torch.int32, device=x.device)
+    check(lib().fmoe_topk_softmax(ptr(x), M, E, topk, int(renormalize), ptr(w), ptr(ids),
+                                  stream_of(x)), "topk_softmax")
+    return w, ids
+
+
+def grouped_topk(gating_output: torch.Tensor, topk: int, num_expert_group: int,
+                 topk_group: int, correction_bias: Optional[torch.Tensor] = None,
+                 renormalize: bool = True, scoring_func: str = "sigmoid"):
+    """DeepSeek-V3 grouped top-k (SGLang biased_grouped_topk semantics)."""
+    require_cuda(gating_output, correction_bias)
+    if scoring_func not in ("sigmoid", "softmax"):
+        raise ValueError(f"Unsupported scoring function: {scoring_func}")
+    x = gating_output.float().contiguous()
+    b = None if correction_bias is None else correction_bias.float().contiguous()
+    M, E = x.shape
+    w = torch.empty(M, topk, dtype=torch.float32, device=x.device)
+    ids = torch.empty(M, topk, dtype=torch.int32, device=x.device)
+    check(lib().fmoe_grouped_topk(ptr(x), ptr(b), M, E, topk, num_expert_group, topk_group,
+                                  0 if scoring_func == "sigmoid" else 1, int(renormalize),
+                                  ptr(w), ptr(ids), stream_of(x)), "grouped_topk")
+    return w, ids
+
+
+# ---------------------------------------------------------------------------
+# alignment
+# ---------------------------------------------------------------------------
+@dataclass
+class _Align:
+    expt_indx: torch.Tensor
+    expt_scal: torch.Tensor
+    topk_indx: torch.Tensor
+    gate_indx: torch.Tensor
+    gate_scal: torch.Tensor
+    hist: torch.Tensor
+    offs_raw: torch.Tensor
+    offs_pad: torch.Tensor
+    tile_map: torch.Tensor
+    n_tiles: torch.Tensor
+    sorted_token_ids: Optional[torch.Tensor]
+    expert_ids: Optional[torch.Tensor]
+    num_tokens_post_padded: Optional[torch.Tensor]
+    block_m: int
+
+
+def _ids_i32(topk_ids: torch.Tensor) -> torch.Tensor:
+    return topk_ids if topk_ids.dtype == torch.int32 and topk_ids.is_contiguous() else \
+        topk_ids.to(torch.int32).contiguous()
+
+
+def _align(topk_weights, topk_ids, n_experts: int, block_m: int, sglang_format: bool) -> _Align:
+    require_cuda(topk_weights, topk_ids)
+    L = lib()
+    ids = _ids_i32(topk_ids)
+    w = topk_weights.float().contiguous()
+    M, k = ids.shape
+    n = M * k
+    dev = ids.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    max_tiles = L.fmoe_max_tiles(n, n_experts)
+    a = _Align(
+        expt_indx=torch.empty(n, **i32), expt_scal=torch.empty(n, dtype=torch.float32, device=dev),
+        topk_indx=torch.empty(n, **i32), gate_indx=torch.empty(n, **i32),
+        gate_scal=torch.empty(n, dtype=torch.float32, device=dev), hist=torch.empty(n_experts, **i32),
+        offs_raw=torch.empty(n_experts + 1, **i32), offs_pad=torch.empty(n_experts + 1, **i32),
+        tile_map=torch.empty(max_tiles, **i32), n_tiles=torch.empty(1, **i32),
+        sorted_token_ids=None, expert_ids=None, num_tokens_post_padded=None, block_m=block_m)
+    if sglang_format:
+        cap = L.fmoe_sorted_ids_len(n, n_experts, block_m)
+        a.sorted_token_ids = torch.empty(cap, **i32)
+        a.expert_ids = torch.empty(cap // block_m + 1, **i32)
+        a.num_tokens_post_padded = torch.empty(1, **i32)
+    o = _lib.AlignOut(*[ptr(getattr(a, f)) for f, _ in _lib.AlignOut._fields_])
+    ws_bytes = L.fmoe_align_workspace_bytes(M, k, n_experts)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    check(L.fmoe_align(ptr(ids), ptr(w), M, k, n_experts, block_m, ctypes.byref(o), ptr(ws),
+                       ws_bytes, stream_of(ids)), "moe_align")
+    return a
+
+
+def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: int):
+    """SGLang ``moe_align_block_size``: returns ``(sorted_token_ids, expert_ids,
+    num_tokens_post_padded)``; token order inside an expert is ascending
+    (stable), padding uses the sentinel ``topk_ids.numel()``."""
+    w = torch.zeros(topk_ids.shape, dtype=torch.float32, device=topk_ids.device)
+    a = _align(w, topk_ids, num_experts, block_size, sglang_format=True)
+    return a.sorted_token_ids, a.expert_ids, a.num_tokens_post_padded
+
+
+def _standard_topk_to_triton_kernels(topk_weights, topk_ids, n_expts_tot, block_m: Optional[int] = None):
+    """Convert standard top-k output to routing data (ops/fused_moe.py:103-130).
+
+    The expert-sorted permutation, its inverse, the sorted gate weights, the
+    histogram and ExptData come from one HIP alignment pass.  ExptData holds
+    the tile map for ``block_m`` (default: the tile height the GEMMs will use);
+    other tile heights are derived from the histogram on demand."""
+    M, k = topk_ids.shape
+    if block_m is None:
+        block_m = lib().fmoe_choose_block_m(W_BF16, M, k, n_expts_tot, 0)
+    a = _align(topk_weights, topk_ids, n_expts_tot, block_m, sglang_format=False)
+    ed = ExptData(hist=a.hist, token_offs_raw=a.offs_raw, token_offs_pad={block_m: a.offs_pad},
+                  block_pid_map={block_m: a.tile_map}, n_tiles={block_m: a.n_tiles})
+    routing_data = RoutingData(a.gate_scal, a.hist, n_expts_tot, k, ed)
+    gather_indx = GatherIndx(src_indx=a.topk_indx, dst_indx=a.gate_indx)
+    scatter_indx = ScatterIndx(src_indx=a.gate_indx, dst_indx=a.topk_indx)
+    return routing_data, gather_indx, scatter_indx
+
+
+def _expt_data_for(routing_data: RoutingData, n_slots: int, block_m: int):
+    """(offs_raw, tile_map, n_tiles) for ``block_m``: reuse the routing's own
+    ExptData when it has this tile height, else derive it from the histogram
+    (compute_expt_data_torch, ops/fused_moe.py:124)."""
+    ed = routing_data.expt_data
+    if ed is not None and block_m in getattr(ed, "block_pid_map", {}) and block_m in getattr(ed, "n_tiles", {}):
+        return ed.token_offs_raw, ed.block_pid_map[block_m], ed.n_tiles[block_m]
+    L = lib()
+    E = routing_data.n_expts_tot
+    hist = routing_data.expt_hist.to(torch.int32).contiguous()
+    dev = hist.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    offs_raw = torch.empty(E + 1, **i32)
+    offs_pad = torch.empty(E + 1, **i32)
+    tile_map = torch.empty(L.fmoe_max_tiles(n_slots, E), **i32)
+    n_tiles = torch.empty(1, **i32)
+    check(L.fmoe_expt_data(ptr(hist), E, n_slots, block_m, ptr(offs_raw), ptr(offs_pad),
+                           ptr(tile_map), ptr(n_tiles), stream_of(hist)), "expt_data")
+    if ed is not None and hasattr(ed, "block_pid_map") and isinstance(ed.block_pid_map, dict):
+        ed.token_offs_pad[block_m] = offs_pad
+        ed.block_pid_map[block_m] = tile_map
+        if isinstance(getattr(ed, "n_tiles", None), dict):
+            ed.n_tiles[block_m] = n_tiles
+    return offs_raw, tile_map, n_tiles
+
+
+# ---------------------------------------------------------------------------
+# quantization
+# ---------------------------------------------------------------------------
+def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128):
+    """Dynamic 1 x group fp8-e4m3fn activation quant: ``(q, scale)`` with
+    ``scale = max(amax, 1e-10) / 448`` per group."""
+    require_cuda(x)
+    x = x.contiguous()
+    if x.dtype != torch.bfloat16:
+        raise ValueError("per_token_group_quant_fp8: x must be bfloat16")
+    M, K = x.shape
+    q = torch.empty(M, K, dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty(M, K // group_size, dtype=torch.float32, device=x.device)
+    check(lib().fmoe_quant_fp8_group(ptr(x), M, K, group_size, ptr(q), ptr(s), stream_of(x)),
+          "per_token_group_quant_fp8")
+    return q, s
+
+
+# ---------------------------------------------------------------------------
+# GEMM stages over reference-format routing
+# ---------------------------------------------------------------------------
+def _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w1_zp, w2_zp,
+                     block_shape, per_channel_quant):
+    assert per_channel_quant is False, _UNSUPPORTED_FEATURE_MSG.format(name="per_channel_quant")
+    if use_fp8_w8a8 and use_int4_w4a16:
+        raise ValueError("use_fp8_w8a8 and use_int4_w4a16 are exclusive")
+    if use_fp8_w8a8:
+        assert block_shape is not None and list(block_shape) == [128, 128], \
+            _UNSUPPORTED_FEATURE_MSG.format(name=f"block_shape={block_shape}")
+        assert w1.dtype == torch.float8_e4m3fn and w2.dtype == torch.float8_e4m3fn, \
+            "fp8 weights must be float8_e4m3fn"
+        assert w1_scale is not None and w2_scale is not None, "fp8 needs w1_scale and w2_scale"
+        return W_FP8
+    if use_int4_w4a16:
+        assert block_shape is None or list(block_shape) in ([0, 128], [128]), \
+            _UNSUPPORTED_FEATURE_MSG.format(name=f"block_shape={block_shape}")
+        assert w1.dtype == torch.uint8 and w2.dtype == torch.uint8, "int4 weights are packed uint8"
+        assert w1_scale is not None and w2_scale is not None and w1_zp is not None and w2_zp is not None, \
+            "int4 needs w1_scale, w2_scale, w1_zp and w2_zp"
+        return W_INT4
+    assert w1_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="w1_scale")
+    assert w2_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="w2_scale")
+    assert block_shape is None, _UNSUPPORTED_FEATURE_MSG.format(name="block_shape")
+    assert w1.dtype == torch.bfloat16, "w1 must be bfloat16"
+    assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
+    return W_BF16
+
+
+def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens, top_k,
+                n_experts, topk_indx, gate_indx, gate_scal, offs_raw, tile_map, n_tiles, block_m,
+                apply_router_weight_on_input, scale, combine=True):
+    """GEMM1+SiLU -> GEMM2 -> top-k sum on prepared routing, SGLang layouts
+    ``w13 [E, 2N, K]``, ``w2 [E, K, N]``."""
+    L = lib()
+    M, K = x.shape
+    N = w2.shape[2] * (2 if wtype == W_INT4 else 1)
+    dev = x.device
+    st = stream_of(x)
+    r = _lib.Routing(ptr(topk_indx), ptr(gate_indx), ptr(gate_scal), ptr(offs_raw), ptr(tile_map),
+                     ptr(n_tiles), n_tokens, top_k, n_experts, block_m,
+                     L.fmoe_max_tiles(n_tokens * top_k, n_experts))
+    slots = n_tokens * top_k
+    xa, xs = x, None
+    if wtype == W_FP8:
+        xa, xs = per_token_group_quant_fp8(x, 128)
+    act = torch.empty(slots, N, dtype=torch.bfloat16, device=dev)
+    check(L.fmoe_gemm1(wtype, ptr(xa), ptr(xs), ptr(w13), ptr(w13_scale), ptr(w13_zp), K, N,
+                       ctypes.byref(r), int(apply_router_weight_on_input), ptr(act), 0, st), "gemm1")
+    a2, a2s = act, None
+    if wtype == W_FP8:
+        a2, a2s = per_token_group_quant_fp8(act, 128)
+    splits = L.fmoe_gemm2_splits(wtype, K, N, ctypes.byref(r), 0)
+    y = torch.empty(splits, slots, K, dtype=torch.float32, device=dev)
+    check(L.fmoe_gemm2(wtype, ptr(a2), ptr(a2s), ptr(w2), ptr(w2_scale), ptr(w2_zp), K, N,
+                       ctypes.byref(r), int(not apply_router_weight_on_input), ptr(y), splits, 0, st),
+          "gemm2")
+    if not combine:
+        # per-slot rows, token-major (each token's experts ascending)
+        yy = y.sum(0) if splits > 1 else y[0]
+        return yy.index_select(0, gate_indx.long()).view(n_tokens, top_k, K).to(torch.bfloat16)
+    out = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
+    check(L.fmoe_moe_sum(ptr(y), splits, ptr(gate_indx), M, top_k, K, float(scale), ptr(out), st),
+          "moe_sum")
+    return out
+
+
+def _as_sglang_layout(w: torch.Tensor) -> torch.Tensor:
+    """matmul_ogs layout [E, K_in, N_out] -> kernel layout [E, N_out, K_in].
+    A transposed view of a contiguous SGLang tensor is used as is; a truly
+    [E, K_in, N_out]-contiguous tensor is transposed once here (the reference
+    pays the same copy in fused_moe_flagos, ops/fused_moe.py:326-327)."""
+    t = w.transpose(-1, -2)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def triton_kernel_fused_experts(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    w2: torch.Tensor,
+    routing_data,
+    gather_indx,
+    scatter_indx,
+    inplace: bool = False,
+    activation: str = "silu",
+    apply_router_weight_on_input: bool = False,
+    use_fp8_w8a8: bool = False,
+    per_channel_quant: bool = False,
+    global_num_experts: int = -1,
+    expert_map: Optional[torch.Tensor] = None,
+    w1_scale: Optional[torch.Tensor] = None,
+    w2_scale: Optional[torch.Tensor] = None,
+    a1_scale: Optional[torch.Tensor] = None,
+    a2_scale: Optional[torch.Tensor] = None,
+    block_shape: Optional[list[int]] = None,
+) -> torch.Tensor:
+    """Drop-in for ``triton_kernel_fused_experts`` (ops/fused_moe.py:133-216).
+
+    ``w1 [E, K, 2N]`` and ``w2 [E, N, K]`` in matmul_ogs layout (or transposed
+    views of SGLang-layout tensors); routing objects as built by
+    ``_standard_topk_to_triton_kernels``.  With ``use_fp8_w8a8`` and
+    ``block_shape=[128, 128]`` the fp8 block path runs (weights fp8 in the same
+    layouts, scales ``[E, 2N/128, K/128]`` / ``[E, K/128, N/128]``); the
+    reference asserts this off.  ``scatter_indx=None`` returns the per-slot
+    outputs ``[M, k, K]`` (token-major, experts ascending) without combining.
+    """
+    logger.debug("FLAGGEMS_SGLANG FUSED_MOE")
+    assert expert_map is None, _UNSUPPORTED_FEATURE_MSG.format(name="expert_map")
+    assert a1_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="a1_scale")
+    assert a2_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="a2_scale")
+    assert inplace is False, "Inplace is not supported"
+    if not use_fp8_w8a8:
+        assert w1_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="w1_scale")
+        assert w2_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="w2_scale")
+        assert block_shape is None, _UNSUPPORTED_FEATURE_MSG.format(name="block_shape")
+    assert hidden_states.ndim == 2, "hidden_states must be 2D"
+    assert hidden_states.dtype == torch.bfloat16, "hidden_states must be bfloat16"
+    if not use_fp8_w8a8:
+        assert w1.dtype == torch.bfloat16, "w1 must be bfloat16"
+        assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
+    assert hidden_states.shape[-1] == w1.shape[-2], "hidden size mismatch"
+    assert w2.shape[-1] == w1.shape[1], "intermediate size mismatch"
+    if activation != "silu":
+        raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+    wtype = _wtype_and_check(use_fp8_w8a8, False, w1, w2, w1_scale, w2_scale, None, None,
+                             block_shape, per_channel_quant)
+    require_cuda(hidden_states, w1, w2)
+
+    x = hidden_states.contiguous()
+    M = x.shape[0]
+    k = routing_data.n_expts_act
+    E = routing_data.n_expts_tot
+    w13 = _as_sglang_layout(w1)
+    w2t = _as_sglang_layout(w2)
+    s13 = None if w1_scale is None else _as_sglang_layout(w1_scale)
+    s2 = None if w2_scale is None else _as_sglang_layout(w2_scale)
+    bm = lib().fmoe_choose_block_m(wtype, M, k, E, 0)
+    offs_raw, tile_map, n_tiles = _expt_data_for(routing_data, M * k, bm)
+    topk_indx = gather_indx.src_indx.to(torch.int32).contiguous()
+    gate_indx = gather_indx.dst_indx.to(torch.int32).contiguous()
+    gate_scal = routing_data.gate_scal.float().contiguous()
+    return _run_stages(x, w13, w2t, wtype, s13, s2, None, None, M, k, E, topk_indx, gate_indx,
+                       gate_scal, offs_raw, tile_map, n_tiles, bm, apply_router_weight_on_input,
+                       1.0, combine=scatter_indx is not None)
+
+
+def triton_kernel_fused_experts_with_bias(*args, **kwargs):
+    """gpt-oss style bias + swiglu variant (ops/fused_moe.py:219-309): not built."""
+    raise AssertionError(_UNSUPPORTED_FEATURE_MSG.format(name="fused experts with bias"))
+
+
+# ---------------------------------------------------------------------------
+# plain-tensor entry point (SGLang fused_experts style, SGLang layouts)
+# ---------------------------------------------------------------------------
+_ws_cache: dict = {}
+
+
+def fused_experts(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    w2: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    inplace: bool = False,
+    activation: str = "silu",
+    apply_router_weight_on_input: bool = False,
+    use_fp8_w8a8: bool = False,
+    use_int4_w4a16: bool = False,
+    per_channel_quant: bool = False,
+    w1_scale: Optional[torch.Tensor] = None,
+    w2_scale: Optional[torch.Tensor] = None,
+    w1_zp: Optional[torch.Tensor] = None,
+    w2_zp: Optional[torch.Tensor] = None,
+    a1_scale: Optional[torch.Tensor] = None,
+    a2_scale: Optional[torch.Tensor] = None,
+    block_shape: Optional[list[int]] = None,
+    routed_scaling_factor: Optional[float] = None,
+    no_combine: bool = False,
+    path: int = 0,
+) -> torch.Tensor:
+    """Whole fused MoE in one C call (align -> GEMM1+SiLU -> GEMM2 -> top-k sum).
+
+    Layouts (SGLang layer): ``w1 [E, 2N, K]``, ``w2 [E, K, N]``;
+      fp8  (``use_fp8_w8a8``, ``block_shape=[128,128]``): float8_e4m3fn weights,
+           ``w1_scale [E, 2N/128, K/128]``, ``w2_scale [E, K/128, N/128]`` fp32;
+           activations quantized per 1x128 group inside the call;
+      int4 (``use_int4_w4a16``, group 128): ``w1 [E, 2N, K/2]`` / ``w2 [E, K, N/2]``
+           uint8 (two uint4 per byte, low nibble first), ``w1_scale [E, K/128, 2N]``
+           / ``w2_scale [E, N/128, K]`` fp16, ``w1_zp [E, K/128, N]`` /
+           ``w2_zp [E, N/128, K/2]`` uint8 (two uint4 zeros per byte).
+    ``path``: 0 choose, 1 prefill kernels, 2 decode kernels.
+    """
+    assert inplace is False, "Inplace is not supported"
+    assert a1_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="a1_scale")
+    assert a2_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="a2_scale")
+    if activation != "silu":
+        raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+    assert hidden_states.ndim == 2 and hidden_states.dtype == torch.bfloat16, \
+        "hidden_states must be 2D bfloat16"
+    wtype = _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w1_zp,
+                             w2_zp, block_shape, per_channel_quant)
+    require_cuda(hidden_states, w1, w2, topk_weights, topk_ids, w1_scale, w2_scale, w1_zp, w2_zp)
+    x = hidden_states.contiguous()
+    M, K = x.shape
+    E = w1.shape[0]
+    k = topk_ids.shape[1]
+    N = w2.shape[2] * (2 if wtype == W_INT4 else 1)
+    kin = w1.shape[2] * (2 if wtype == W_INT4 else 1)
+    assert kin == K and w1.shape[1] == 2 * N and w2.shape[1] == K, "weight shapes do not match"
+    for t in (w1, w2, w1_scale, w2_scale, w1_zp, w2_zp):
+        if t is not None:
+            assert t.is_contiguous(), "weights and scales must be contiguous"
+    scale = 1.0 if routed_scaling_factor is None else float(routed_scaling_factor)
+    if no_combine:
+        a = _align(topk_weights, topk_ids, E, lib().fmoe_choose_block_m(wtype, M, k, E, path), False)
+        return _run_stages(x, w1, w2, wtype, w1_scale, w2_scale, w1_zp, w2_zp, M, k, E,
+                           a.topk_indx, a.gate_indx, a.gate_scal, a.offs_raw, a.tile_map, a.n_tiles,
+                           a.block_m, apply_router_weight_on_input, 1.0, combine=False)
+    ids = _ids_i32(topk_ids)
+    tw = topk_weights.float().contiguous()
+    out = torch.empty(M, K, dtype=torch.bfloat16, device=x.device)
+    args = _lib.FusedArgs(
+        wtype, ptr(x), M, K, N, E, k, ptr(w1), ptr(w2), ptr(w1_scale), ptr(w2_scale), ptr(w1_zp),
+        ptr(w2_zp), 128, ptr(tw), ptr(ids), int(apply_router_weight_on_input), scale, path,
+        ptr(out), None, 0)
+    L = lib()
+    nbytes = L.fmoe_fused_experts_workspace_bytes(ctypes.byref(args))
+    if nbytes == 0:
+        check(L.fmoe_fused_experts(ctypes.byref(args), stream_of(x)), "fused_experts")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    args.workspace = ptr(ws)
+    args.workspace_bytes = nbytes
+    check(L.fmoe_fused_experts(ctypes.byref(args), stream_of(x)), "fused_experts")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# SGLang runner hook
+# ---------------------------------------------------------------------------
+def _combine_input(hidden_states):
+    try:
+        from sglang.srt.layers.moe.token_dispatcher.standard import StandardCombineInput
+    except Exception:
+        return CombineInput(hidden_states=hidden_states)
+    return StandardCombineInput(hidden_states=hidden_states)
+
+
+def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
+    """SGLang integration wrapper (ops/fused_moe.py:312-406).
+
+    Reads the same fields: ``layer.w13_weight [E, 2N, K]`` and
+    ``layer.w2_weight [E, K, N]`` (used in place, no per-call transpose),
+    optional ``w13_weight_bias``/``w2_weight_bias`` (bias path: not built),
+    ``dispatch_output.hidden_states`` and ``.topk_output`` (either
+    ``topk_weights``/``topk_ids`` or a triton_kernels-format
+    ``(routing_data, gather_indx, scatter_indx)`` triple), and
+    ``obj.runner.config`` (``num_experts``, ``no_combine``, ``activation``,
+    ``apply_router_weight_on_input``, ``routed_scaling_factor``).
+    fp8 block-scale layers carry ``w13_weight_scale_inv``/``w2_weight_scale_inv``;
+    int4 layers ``w13_qweight``/``w13_scales``/``w13_qzeros`` and the w2 ones.
+    """
+    cfg = obj.runner.config
+    if getattr(layer, "w13_weight_bias", None) is not None or getattr(layer, "w2_weight_bias", None) is not None:
+        raise AssertionError(_UNSUPPORTED_FEATURE_MSG.format(name="fused experts with bias"))
+    hidden_states = dispatch_output.hidden_states
+    topk_output = dispatch_output.topk_output
+    no_combine = bool(getattr(cfg, "no_combine", False))
+    rsf = getattr(cfg, "routed_scaling_factor", None)
+    scale = None if (rsf is None or rsf == 1.0 or no_combine) else rsf
+    activation = getattr(cfg, "activation", "silu")
+    on_input = bool(getattr(cfg, "apply_router_weight_on_input", False))
+
+    if hasattr(layer, "w13_qweight"):
+        quant = dict(use_int4_w4a16=True, w1_scale=layer.w13_scales, w2_scale=layer.w2_scales,
+                     w1_zp=layer.w13_qzeros, w2_zp=layer.w2_qzeros)
+        w13, w2 = layer.w13_qweight, layer.w2_qweight
+    elif getattr(layer, "w13_weight_scale_inv", None) is not None:
+        quant = dict(use_fp8_w8a8=True, block_shape=[128, 128], w1_scale=layer.w13_weight_scale_inv,
+                     w2_scale=layer.w2_weight_scale_inv)
+        w13, w2 = layer.w13_weight, layer.w2_weight
+    else:
+        quant = {}
+        w13, w2 = layer.w13_weight, layer.w2_weight
+
+    if isinstance(topk_output, tuple) and len(topk_output) == 3 and isinstance(topk_output[0], RoutingData):
+        routing_data, gather_indx, scatter_indx = topk_output
+        assert not quant.get("use_int4_w4a16"), _UNSUPPORTED_FEATURE_MSG.format(
+            name="int4 with triton_kernels routing")
+        out = triton_kernel_fused_experts(
+            hidden_states, w13.transpose(-1, -2), w2.transpose(-1, -2), routing_data, gather_indx,
+            None if no_combine else scatter_indx, activation=activation,
+            apply_router_weight_on_input=on_input,
+            use_fp8_w8a8=bool(quant.get("use_fp8_w8a8")),
+            w1_scale=None if not quant else quant["w1_scale"].transpose(-1, -2),
+            w2_scale=None if not quant else quant["w2_scale"].transpose(-1, -2),
+            block_shape=quant.get("block_shape"))
+        if scale is not None:
+            out.mul_(scale)
+    else:
+        out = fused_experts(
+            hidden_states, w13, w2, topk_output.topk_weights, topk_output.topk_ids,
+            activation=activation, apply_router_weight_on_input=on_input,
+            routed_scaling_factor=scale, no_combine=no_combine, **quant)
+    return _combine_input(out)

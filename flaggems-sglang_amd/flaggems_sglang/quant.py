@@ -1,0 +1,54 @@
+"""Weight preparation for the quantized fused-MoE paths (load time, not the
+hot path): fp8-e4m3fn 128x128 block quantization and uint4 group
+quantization into the layouts ``fused_experts`` reads.  Plain torch, on
+whatever device the weights live.
+"""
+
+from __future__ import annotations
+
+import torch
+
+FP8_MAX = 448.0
+FP8_EPS = 1e-10
+
+
+def quantize_fp8_block(w: torch.Tensor, block=(128, 128)):
+    """``w [E, R, C]`` -> (float8_e4m3fn ``[E, R, C]``, fp32 scales
+    ``[E, R/bR, C/bC]``) with scale = max(amax, 1e-10) / 448 per block."""
+    E, R, C = w.shape
+    bR, bC = block
+    if R % bR or C % bC:
+        raise ValueError(f"quantize_fp8_block: {R}x{C} is not a multiple of {bR}x{bC}")
+    wf = w.float().view(E, R // bR, bR, C // bC, bC)
+    s = wf.abs().amax(dim=(2, 4)).clamp_min(FP8_EPS) / FP8_MAX
+    q = (wf / s[:, :, None, :, None]).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q.view(E, R, C), s
+
+
+def _pack_u4(q: torch.Tensor) -> torch.Tensor:
+    if q.shape[-1] % 2:
+        q = torch.nn.functional.pad(q, (0, 1))
+    return (q[..., 0::2] | (q[..., 1::2] << 4)).contiguous()
+
+
+def quantize_int4_group(w: torch.Tensor, group: int = 128):
+    """Asymmetric uint4 quantization of ``w [E, R, C]`` in groups of ``group``
+    along C (the reduction dim).
+
+    scale = fp16((max - min) / 15, floored at 1e-8), zero = clamp(round(-min /
+    scale), 0, 15), q = clamp(round(w / scale) + zero, 0, 15).  Returns
+    ``(qweight [E, R, C/2] u8, scales [E, C/group, R] fp16, zeros
+    [E, C/group, ceil(R/2)] u8)``; two nibbles per byte, low nibble first."""
+    E, R, C = w.shape
+    if C % group:
+        raise ValueError(f"quantize_int4_group: {C} is not a multiple of {group}")
+    G = C // group
+    wf = w.float().view(E, R, G, group)
+    mn = wf.amin(dim=-1)
+    mx = wf.amax(dim=-1)
+    sc = ((mx - mn) / 15.0).clamp_min(1e-8).to(torch.float16)
+    scf = sc.float()
+    z = torch.clamp(torch.round(-mn / scf), 0, 15)
+    q = torch.clamp(torch.round(wf / scf[..., None]) + z[..., None], 0, 15).to(torch.uint8)
+    return (_pack_u4(q.view(E, R, C)), sc.transpose(1, 2).contiguous(),
+            _pack_u4(z.to(torch.uint8).transpose(1, 2).contiguous()))

@@ -1,0 +1,229 @@
+/*
+ * fmoe.h — C ABI of the MI355X (gfx950) fused-MoE library `libfmoe.so`.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream passed
+ * as `void*` (a hipStream_t; NULL = the default stream), enqueues its kernels
+ * on that stream and returns a status code without synchronising.  Nothing
+ * here allocates device memory: buffers, including workspaces whose size the
+ * matching *_bytes() query reports, belong to the caller.  Calls are
+ * re-entrant; concurrent calls must not share output or workspace buffers.
+ *
+ * Reference interfaces each entry replaces are cited as path:line relative to
+ * the FlagGems-sglang source root (src/flaggems_sglang/...).
+ *
+ * Tensor layouts (row-major, contiguous):
+ *   hidden states x      [M, K]          bf16 (fp8 path: quantized in-library)
+ *   w13 (gate ; up)      [E, 2N, K]      bf16 | fp8-e4m3fn | uint4 packed [E, 2N, K/2]
+ *   w2                   [E, K, N]       bf16 | fp8-e4m3fn | uint4 packed [E, K, N/2]
+ *   fp8 weight scales    w13 [E, 2N/128, K/128], w2 [E, K/128, N/128]   fp32
+ *   int4 scales          w13 [E, K/g, 2N] fp16, w2 [E, N/g, K] fp16    (group g)
+ *   int4 zeros           w13 [E, K/g, N]  u8 (2 per byte), w2 [E, N/g, K/2] u8
+ *   topk_ids/topk_weights [M, k]         int32 / fp32
+ *   output               [M, K]          bf16
+ * "slots" are the M*k (token, expert) pairs; the routing below orders them by
+ * expert (stable: ascending token within an expert).
+ */
+#ifndef FMOE_H_
+#define FMOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ status codes */
+enum fmoe_status {
+  FMOE_OK = 0,
+  FMOE_ERR_INVALID = 1,     /* bad pointer / shape / value (reference: assert) */
+  FMOE_ERR_UNSUPPORTED = 2, /* feature or shape not implemented ("... is not supported") */
+  FMOE_ERR_WORKSPACE = 3,   /* workspace smaller than the *_bytes() query */
+  FMOE_ERR_HIP = 4,         /* a HIP runtime / launch error */
+};
+
+enum fmoe_wtype {
+  FMOE_W_BF16 = 0,     /* bf16 weights, bf16 activations */
+  FMOE_W_FP8 = 1,      /* fp8 e4m3fn weights with 128x128 block scales, 1x128 dynamic activation quant */
+  FMOE_W_INT4 = 2,     /* uint4 weights with fp16 group scales and uint4 zeros, bf16 activations */
+};
+
+/* Text of a status code, and the message of the last failure on this thread. */
+const char* fmoe_status_string(int status);
+const char* fmoe_last_error(void);
+int fmoe_abi_version(void);
+
+/* --------------------------------------------------------------- routing
+ * Router: logits [M, E] fp32 -> topk_weights [M, k] fp32, topk_ids [M, k]
+ * int32, in descending score order.
+ *
+ * fmoe_topk_softmax replaces the softmax -> torch.topk -> renormalise
+ * sequence of tests/test_fused_moe.py:24-27 (SGLang's fused_topk).
+ * Requires 1 <= k <= 32, k <= E <= 1024.
+ */
+int fmoe_topk_softmax(const float* logits, int64_t M, int E, int k, int renormalize,
+                      float* topk_weights, int32_t* topk_ids, void* stream);
+
+/* Grouped top-k (DeepSeek-V3 routing; SGLang biased_grouped_topk, external to
+ * the reference): scores = sigmoid(logits) (scoring 0) or softmax (1);
+ * selection on scores + bias (bias may be NULL); group score = sum of top-2
+ * in each of n_group groups; the topk_group best groups are kept; k experts
+ * picked by biased score; weights are the unbiased scores, renormalised.
+ * Requires E % n_group == 0, E / n_group >= 2, E <= 1024, n_group <= 64. */
+int fmoe_grouped_topk(const float* logits, const float* bias, int64_t M, int E, int k,
+                      int n_group, int topk_group, int scoring, int renormalize,
+                      float* topk_weights, int32_t* topk_ids, void* stream);
+
+/* ------------------------------------------------------------- alignment
+ * Replaces _standard_topk_to_triton_kernels (ops/fused_moe.py:103-130) plus
+ * triton_kernels.routing.compute_expt_data_torch (called at :124) and
+ * SGLang's moe_align_block_size, in one deterministic pass (histogram ->
+ * exclusive scan -> stable scatter).  Outputs (device, caller-allocated):
+ *
+ *   expt_indx   [M*k]  int32  per-token ascending expert ids, flattened (:114-117)
+ *   expt_scal   [M*k]  fp32   weights gathered alongside (:115-116)
+ *   topk_indx   [M*k]  int32  expert-sorted slot -> flat index (:118)
+ *   gate_indx   [M*k]  int32  inverse permutation (:119)
+ *   gate_scal   [M*k]  fp32   weight of each sorted slot (:120)
+ *   hist        [E]    int32  slots per expert (:121-123)
+ *   offs_raw    [E+1]  int32  ExptData.token_offs_raw
+ *   offs_pad    [E+1]  int32  ExptData.token_offs_pad[block_m] (in tiles)
+ *   tile_map    [fmoe_max_tiles()] int32  ExptData.block_pid_map[block_m]:
+ *                              (tile_in_expert << 16) | expert, -1 unused
+ *   n_tiles     [1]    int32  used tiles
+ *   sorted_token_ids [fmoe_sorted_ids_len()] int32 (may be NULL): SGLang
+ *              moe_align_block_size format, flat indices of topk_ids, padded
+ *              per expert to block_m with the sentinel M*k
+ *   expert_ids [fmoe_sorted_ids_len()/block_m + 1] int32 (may be NULL): expert
+ *              of each block_m block, -1 past the used blocks
+ *   num_tokens_post_padded [1] int32 (may be NULL)
+ *
+ * topk_ids values must lie in [0, E) and be distinct within a row;
+ * FMOE_ERR_INVALID is not detectable for out-of-range ids without a device
+ * sync, so ids >= E are counted into no expert and their slots are dropped
+ * (gate_scal 0, never read by the GEMMs).
+ * Requires 1 <= k <= 32, 1 <= E <= 1024, block_m in {16, 32, 64, 128}.
+ */
+typedef struct fmoe_align_out {
+  int32_t* expt_indx;
+  float* expt_scal;
+  int32_t* topk_indx;
+  int32_t* gate_indx;
+  float* gate_scal;
+  int32_t* hist;
+  int32_t* offs_raw;
+  int32_t* offs_pad;
+  int32_t* tile_map;
+  int32_t* n_tiles;
+  int32_t* sorted_token_ids;
+  int32_t* expert_ids;
+  int32_t* num_tokens_post_padded;
+} fmoe_align_out;
+
+int64_t fmoe_max_tiles(int64_t n_slots, int E);
+int64_t fmoe_sorted_ids_len(int64_t n_slots, int E, int block_m);
+size_t fmoe_align_workspace_bytes(int64_t M, int k, int E);
+int fmoe_align(const int32_t* topk_ids, const float* topk_weights, int64_t M, int k, int E,
+               int block_m, const fmoe_align_out* out, void* workspace, size_t workspace_bytes,
+               void* stream);
+
+/* ExptData from a histogram alone (compute_expt_data_torch; used when the
+ * caller already holds triton_kernels-format routing, ops/fused_moe.py:339-340). */
+int fmoe_expt_data(const int32_t* hist, int E, int64_t n_slots, int block_m, int32_t* offs_raw,
+                   int32_t* offs_pad, int32_t* tile_map, int32_t* n_tiles, void* stream);
+
+/* ------------------------------------------------------------ quantization
+ * Dynamic per-token-group fp8 quant (SGLang per_token_group_quant_fp8):
+ * scale = max(amax, 1e-10) / 448, q = e4m3fn(clamp(x / scale, +-448)) (RNE).
+ * x [M, K] bf16 -> q [M, K] fp8, scale [M, K/group] fp32.  K % group == 0,
+ * group in {64, 128}. */
+int fmoe_quant_fp8_group(const void* x, int64_t M, int64_t K, int group, void* q, float* scale,
+                         void* stream);
+
+/* ------------------------------------------------------------------- GEMMs
+ * Routing view the GEMMs read (all device pointers from fmoe_align /
+ * fmoe_expt_data for the same block_m). */
+typedef struct fmoe_routing {
+  const int32_t* topk_indx;
+  const int32_t* gate_indx;
+  const float* gate_scal;
+  const int32_t* offs_raw;
+  const int32_t* tile_map;
+  const int32_t* n_tiles;
+  int64_t n_tokens;
+  int32_t top_k;
+  int32_t n_experts;
+  int32_t block_m;
+  int32_t max_tiles;
+} fmoe_routing;
+
+/* GEMM1 with fused SiLU*mul: replaces matmul_ogs(x, w1, gather_indx, gammas)
+ * + _silu_and_mul_triton (ops/fused_moe.py:189-202).  For every sorted slot
+ * s of expert e:  inter = bf16(x[token(s)] @ w13[e]^T  [* gate_scal[s] when
+ * gamma_on_input]);  act[s, j] = bf16(silu(inter[j]) * inter[N + j]).
+ * act: [M*k, N] bf16 in sorted-slot order.  fp8: x is fp8 [M, K] with
+ * x_scale [M, K/128]; int4: w13_scale/w13_zero as in the header comment.
+ * Requires K % 128 == 0, N % 128 == 0 (int4: group == 128). */
+int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const void* w13,
+               const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
+               const fmoe_routing* r, int gamma_on_input, void* act, int path, void* stream);
+
+/* GEMM2: replaces matmul_ogs(act, w2, scatter_indx, gammas) up to the top-k
+ * sum (ops/fused_moe.py:208-215): y[split][s, :] = act[s] @ w2[e]^T
+ * [* gate_scal[s] when apply_gamma], fp32, sorted-slot order.  `splits`
+ * partial sums over the reduction dim N are written to y[0..splits-1]
+ * (fmoe_gemm2_splits() gives the count the library picks). */
+int fmoe_gemm2(int wtype, const void* act, const float* act_scale, const void* w2,
+               const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
+               const fmoe_routing* r, int apply_gamma, float* y, int splits, int path,
+               void* stream);
+int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_routing* r, int path);
+
+/* Tile height the library pairs with the GEMM kernels for a problem size:
+ * 16 selects the decode (streaming) kernels, 64 / 128 the prefill kernels.
+ * path: 0 = choose, 1 = prefill, 2 = decode (int4 is decode-only). */
+int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path);
+
+/* Top-k combine (the scatter + sum inside matmul_ogs, ops/fused_moe.py:208-216,
+ * and routed_scaling_factor, :399-404): out[t, :] = bf16(scale *
+ * sum_{j<k} sum_{p<splits} y[p][gate_indx[t*k + j], :]), summed in fixed
+ * order (deterministic). */
+int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx, int64_t M, int k,
+                 int64_t K, float scale, void* out, void* stream);
+
+/* ------------------------------------------------------ whole fused path
+ * One call: align -> [fp8 quant x] -> GEMM1+SiLU -> [fp8 quant act] -> GEMM2
+ * -> top-k sum.  Replaces triton_kernel_fused_experts + the routing
+ * conversion (ops/fused_moe.py:103-216, :341-350, :399-404) with
+ * SGLang-layout weights (no per-call transpose, cf. :326-327).  `path`:
+ * 0 = choose, 1 = prefill (LDS-tiled) kernels, 2 = decode (streaming) kernels.
+ */
+typedef struct fmoe_fused_args {
+  int32_t wtype;
+  const void* x;
+  int64_t M, K, N;
+  int32_t E, top_k;
+  const void* w13;
+  const void* w2;
+  const void* w13_scale;
+  const void* w2_scale;
+  const void* w13_zero;
+  const void* w2_zero;
+  int32_t group_size;
+  const float* topk_weights;
+  const int32_t* topk_ids;
+  int32_t apply_router_weight_on_input;
+  float routed_scaling_factor; /* 1.0 = none */
+  int32_t path;
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+} fmoe_fused_args;
+
+size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a);
+int fmoe_fused_experts(const fmoe_fused_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FMOE_H_ */

@@ -1,0 +1,207 @@
+"""GPU parity of the fused-MoE path against the CPU oracle, through the C ABI.
+
+Mirrors the reference's accuracy tests (tests/test_fused_moe.py:84-113: every
+FUSED_MOE_SHAPES entry, plus apply_router_weight_on_input on the small
+shapes; inputs per its _make_inputs, seed M+K+N+E+topk) and adds the
+BASELINE configurations (bf16, skewed routing, fp8 block-scale, int4) at
+sizes the oracle finishes in seconds.  Tolerances: bf16 atol=rtol=2e-2;
+fp8 / int4 5e-2 against the dequantize-then-compute oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import flaggems_sglang
+from flaggems_sglang import quant as Q
+from flaggems_sglang.ops import fused_moe as F
+from oracle import fused_moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+# tests/accuracy_utils.py:100-118
+FUSED_MOE_SHAPES_SMALL = [(1, 128, 256, 8, 2), (7, 128, 256, 8, 2), (33, 256, 512, 16, 4)]
+FUSED_MOE_SHAPES_LARGE = [(m, 1280, 3072, 64, 8) for m in (1, 4, 17, 64, 1024, 2048, 4096)]
+
+
+def _ref_inputs(M, K, N, E, topk):
+    """The reference's _make_inputs (tests/test_fused_moe.py:50-58), on CPU:
+    x ~ N(0,1) bf16, w1 [E,K,2N] and w2 [E,N,K] ~ N(0,1)*0.1 bf16, logits."""
+    torch.manual_seed(M + K + N + E + topk)
+    x = torch.randn(M, K, dtype=torch.bfloat16)
+    w1 = torch.randn(E, K, N * 2, dtype=torch.bfloat16) * 0.1
+    w2 = torch.randn(E, N, K, dtype=torch.bfloat16) * 0.1
+    logits = torch.randn(M, E, dtype=torch.float32)
+    tw, ti = O.softmax_topk(logits, topk)
+    return x, w1, w2, tw, ti
+
+
+def _close(out, ref, tol):
+    """Elementwise |out - ref| <= tol * rms(ref) + tol * |ref|, and the global
+    relative error ||out - ref|| / ||ref|| below tol / 4.
+
+    The absolute part scales with the output's RMS: both sides round the
+    GEMM1 output and the activation to bf16, so a one-ulp flip there (from a
+    different fp32 summation order) moves an output by about
+    ulp(act) * |w2| * sqrt(#flips) -- proportional to the output scale, not
+    to the value itself (the reference's own shapes, weights N(0,1)*0.1, give
+    outputs of RMS ~10 where a cancelling element can sit near 0)."""
+    out = out.float().cpu()
+    ref = ref.float()
+    rms = float(ref.pow(2).mean().sqrt()) if ref.numel() else 1.0
+    scale = max(rms, 1e-3)
+    torch.testing.assert_close(out, ref, atol=tol * scale, rtol=tol)
+    if ref.numel():
+        rel = float((out - ref).norm() / ref.norm().clamp_min(1e-30))
+        assert rel < tol / 4, f"global relative error {rel:.3e}"
+
+
+@pytest.mark.parametrize("shape", FUSED_MOE_SHAPES_SMALL + FUSED_MOE_SHAPES_LARGE,
+                         ids=lambda s: "M{}_K{}_N{}_E{}_topk{}".format(*s))
+def test_fused_moe(shape):
+    M, K, N, E, topk = shape
+    x, w1, w2, tw, ti = _ref_inputs(M, K, N, E, topk)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw.to(DEV), ti.to(DEV), E)
+    res = flaggems_sglang.triton_kernel_fused_experts(x.to(DEV), w1.to(DEV), w2.to(DEV), rd, gi, si)
+    ref = O.fused_experts(x, w1.transpose(1, 2), w2.transpose(1, 2), tw, ti)
+    _close(res, ref, 2e-2)
+
+
+@pytest.mark.parametrize("shape", FUSED_MOE_SHAPES_SMALL, ids=lambda s: "M{}_K{}_N{}_E{}_topk{}".format(*s))
+def test_fused_moe_input_gate(shape):
+    M, K, N, E, topk = shape
+    x, w1, w2, tw, ti = _ref_inputs(M, K, N, E, topk)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw.to(DEV), ti.to(DEV), E)
+    res = flaggems_sglang.triton_kernel_fused_experts(x.to(DEV), w1.to(DEV), w2.to(DEV), rd, gi, si,
+                                                      apply_router_weight_on_input=True)
+    ref = O.fused_experts(x, w1.transpose(1, 2), w2.transpose(1, 2), tw, ti,
+                          apply_router_weight_on_input=True)
+    _close(res, ref, 2e-2)
+
+
+@pytest.mark.parametrize("path", [1, 2])
+@pytest.mark.parametrize("M", [1, 16, 64, 300])
+def test_fused_experts_both_paths(M, path):
+    """Prefill (LDS-tiled) and decode (streaming) kernels on the same inputs."""
+    K, N, E, k = 512, 384, 16, 4
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), d["w13"].to(DEV), d["w2"].to(DEV),
+                                        d["topk_weights"].to(DEV), d["topk_ids"].to(DEV), path=path)
+    ref = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"])
+    _close(out, ref, 2e-2)
+
+
+def test_tiny_config():
+    """M=64, K=128, N=256, E=8, top-2 (fp32 oracle; the
+    GPU computes in bf16 with fp32 accumulation)."""
+    d = O.make_inputs(64, 128, 256, 8, 2, wscale=0.02)
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), d["w13"].to(DEV), d["w2"].to(DEV),
+                                        d["topk_weights"].to(DEV), d["topk_ids"].to(DEV))
+    ref = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"])
+    _close(out, ref, 2e-2)
+
+
+def test_routed_scaling_and_no_combine():
+    d = O.make_inputs(40, 256, 256, 8, 2, wscale=0.05)
+    args = [d[n].to(DEV) for n in ("x", "w13", "w2", "topk_weights", "topk_ids")]
+    out = flaggems_sglang.fused_experts(*args, routed_scaling_factor=2.5)
+    ref = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"],
+                          routed_scaling_factor=2.5)
+    _close(out, ref, 2e-2)
+    per = flaggems_sglang.fused_experts(*args, no_combine=True)
+    assert per.shape == (40, 2, 256)
+    base = flaggems_sglang.fused_experts(*args)
+    _close(per.float().sum(1), base.float().cpu(), 2e-2)
+
+
+# ------------------------------------------------------------ BASELINE configs
+def _bf16_case(M, K, N, E, k, bias=0.0, seed=None):
+    d = O.make_inputs(M, K, N, E, k, wscale=0.02, expert_bias_std=bias, seed=seed)
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), d["w13"].to(DEV), d["w2"].to(DEV),
+                                        d["topk_weights"].to(DEV), d["topk_ids"].to(DEV))
+    ref = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"])
+    _close(out, ref, 2e-2)
+
+
+@pytest.mark.parametrize("M", [1, 16, 256])
+def test_qwen3_skewed_bf16(M):
+    # E=128 top-8 K=2048 N=768, per-expert bias N(0, 0.5) skews the routing
+    _bf16_case(M, 2048, 768, 128, 8, bias=0.5)
+
+
+def test_mixtral_shape_bf16_small_experts():
+    # Mixtral K/N at M=16 with all 8 experts (weights 2.8 GB bf16)
+    _bf16_case(16, 4096, 14336, 8, 2)
+
+
+@pytest.mark.parametrize("M", [1, 128, 512])
+def test_dsv3_fp8(M):
+    """DeepSeek-V3 shape fp8 W8A8 with 128x128 weight blocks, grouped top-k
+    routing; E reduced to 32 to keep the CPU oracle within seconds (the
+    kernels see the full K=7168, N=2048)."""
+    K, N, E, k = 7168, 2048, 32, 8
+    d = O.make_inputs(M, K, N, E, k, wscale=0.02, routing="grouped", n_group=8, topk_group=4)
+    w13 = d["w13"].to(DEV)
+    w2 = d["w2"].to(DEV)
+    q1, s1 = Q.quantize_fp8_block(w13)
+    q2, s2 = Q.quantize_fp8_block(w2)
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), q1, q2, d["topk_weights"].to(DEV),
+                                        d["topk_ids"].to(DEV), use_fp8_w8a8=True, w1_scale=s1,
+                                        w2_scale=s2, block_shape=[128, 128])
+    ref = O.fused_experts_fp8(d["x"], q1.cpu(), s1.cpu(), q2.cpu(), s2.cpu(), d["topk_weights"],
+                              d["topk_ids"])
+    _close(out, ref, 5e-2)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 64])
+def test_mixtral_w4a16(M):
+    K, N, E, k = 4096, 14336, 8, 2
+    d = O.make_inputs(M, K, N, E, k, wscale=0.02)
+    q1, sc1, z1 = Q.quantize_int4_group(d["w13"].to(DEV))
+    q2, sc2, z2 = Q.quantize_int4_group(d["w2"].to(DEV))
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), q1, q2, d["topk_weights"].to(DEV),
+                                        d["topk_ids"].to(DEV), use_int4_w4a16=True, w1_scale=sc1,
+                                        w2_scale=sc2, w1_zp=z1, w2_zp=z2)
+    ref = O.fused_experts_w4a16(d["x"], q1.cpu(), sc1.cpu(), z1.cpu(), q2.cpu(), sc2.cpu(),
+                                z2.cpu(), d["topk_weights"], d["topk_ids"])
+    _close(out, ref, 5e-2)
+
+
+def test_product_quantizers_match_oracle():
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn(2, 256, 384, generator=g) * 0.02).to(torch.bfloat16)
+    q, s = Q.quantize_fp8_block(w.to(DEV))
+    qo, so = O.block_quant_fp8(w)
+    assert torch.equal(q.cpu().view(torch.uint8), qo.view(torch.uint8)) and torch.equal(s.cpu(), so)
+    a, b, c = Q.quantize_int4_group(w.to(DEV))
+    ao, bo, co = O.quant_int4(w)
+    assert torch.equal(a.cpu(), ao) and torch.equal(b.cpu(), bo) and torch.equal(c.cpu(), co)
+
+
+# --------------------------------------------- full-size, size-independent checks
+def test_mixtral_prefill_permutation_and_determinism():
+    """Mixtral bf16 at M=4096 (the bench workload): outputs are bit-identical
+    across runs, and permuting the tokens permutes the output rows exactly
+    (each row's arithmetic does not depend on its neighbours)."""
+    M, K, N, E, k = 4096, 4096, 14336, 8, 2
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    x = torch.randn(M, K, device=DEV, generator=gen).to(torch.bfloat16)
+    w13 = (torch.randn(E, 2 * N, K, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, K, N, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    logits = torch.randn(M, E, device=DEV, generator=gen)
+    tw, ti = flaggems_sglang.topk_softmax(logits, k)
+    a = flaggems_sglang.fused_experts(x, w13, w2, tw, ti)
+    b = flaggems_sglang.fused_experts(x, w13, w2, tw, ti)
+    assert torch.equal(a, b)
+    perm = torch.randperm(M, device=DEV, generator=gen)
+    c = flaggems_sglang.fused_experts(x[perm], w13, w2, tw[perm], ti[perm])
+    assert torch.equal(c, a[perm])
+    # spot-check 8 tokens against the oracle
+    sel = perm[:8].cpu()
+    xs, ws, ids = x[sel.to(DEV)].cpu(), tw[sel.to(DEV)].cpu(), ti[sel.to(DEV)].cpu()
+    used = sorted(set(ids.flatten().tolist()))
+    remap = {e: i for i, e in enumerate(used)}
+    ids_l = ids.clone().apply_(lambda e: remap[e])
+    ref = O.fused_experts(xs, w13[used].cpu(), w2[used].cpu(), ws, ids_l)
+    _close(a[sel.to(DEV)], ref, 2e-2)

@@ -1,0 +1,62 @@
+"""CPU checks of the host mirror: the reference's argument contract
+(ops/fused_moe.py:154-179, :206) is enforced before any device work."""
+
+import pytest
+import torch
+
+import flaggems_sglang
+from flaggems_sglang.ops import fused_moe as F
+
+
+def _rd():
+    z = torch.zeros(4, dtype=torch.int32)
+    return F.RoutingData(torch.zeros(4), z, 8, 2), F.GatherIndx(z, z), F.ScatterIndx(z, z)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(expert_map=torch.zeros(1)), "expert_map is not supported"),
+    (dict(a1_scale=torch.zeros(1)), "a1_scale is not supported"),
+    (dict(w1_scale=torch.zeros(1)), "w1_scale is not supported"),
+    (dict(block_shape=[128, 128]), "block_shape is not supported"),
+    (dict(per_channel_quant=True), "per_channel_quant is not supported"),
+    (dict(inplace=True), "Inplace is not supported"),
+])
+def test_unsupported_features_assert(kw, msg):
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    w1 = torch.zeros(8, 128, 512, dtype=torch.bfloat16)
+    w2 = torch.zeros(8, 256, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match=msg):
+        flaggems_sglang.triton_kernel_fused_experts(x, w1, w2, *_rd(), **kw)
+
+
+def test_dtype_and_shape_asserts():
+    x = torch.zeros(2, 128, dtype=torch.float32)
+    w1 = torch.zeros(8, 128, 512, dtype=torch.bfloat16)
+    w2 = torch.zeros(8, 256, 128, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError, match="hidden_states must be bfloat16"):
+        flaggems_sglang.triton_kernel_fused_experts(x, w1, w2, *_rd())
+    with pytest.raises(AssertionError, match="hidden size mismatch"):
+        flaggems_sglang.triton_kernel_fused_experts(
+            torch.zeros(2, 64, dtype=torch.bfloat16), w1, w2, *_rd())
+
+
+def test_unknown_activation_raises_value_error():
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    w1 = torch.zeros(8, 128, 512, dtype=torch.bfloat16)
+    w2 = torch.zeros(8, 256, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="Unsupported FusedMoe activation: gelu_tanh"):
+        flaggems_sglang.triton_kernel_fused_experts(x, w1, w2, *_rd(), activation="gelu_tanh")
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    """No CPU fallback: host tensors raise instead of being computed in torch."""
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    w1 = torch.zeros(8, 512, 128, dtype=torch.bfloat16)
+    w2 = torch.zeros(8, 128, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        flaggems_sglang.fused_experts(x, w1, w2, torch.ones(2, 2), torch.zeros(2, 2, dtype=torch.int32))
+
+
+def test_bias_path_not_built():
+    with pytest.raises(AssertionError, match="is not supported"):
+        flaggems_sglang.triton_kernel_fused_experts_with_bias()
