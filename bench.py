@@ -215,8 +215,8 @@ def cpu_baseline(p, budget_s=10.0):
 
     S = min(p["M"], 64)
     t = run(S)
-    if t < budget_s / 2 and S < p["M"]:
-        S = int(min(p["M"], max(S, S * budget_s / max(t, 1e-3))))
+    while t < budget_s / 2 and S < p["M"]:
+        S = int(min(p["M"], max(2 * S, S * budget_s / max(t, 1e-3))))
         t = run(S)
     del used
     f = 6.0 * S * p["k"] * p["K"] * p["N"]
@@ -306,6 +306,9 @@ def main():
     ap.add_argument("--secondary", default="dsv3_fp8_m4096,mixtral_w4a16_m1,mixtral_w4a16_m16",
                     help="comma list of extra workloads reported in 'secondary' ('' for none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run a plain 1 GiB device copy 5x (reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the fused-MoE kernels on one "
@@ -338,17 +341,25 @@ def main():
         "stages_ms": {k: round(v, 4) for k, v in head["stages"].items() if k != "block_m"},
     }
     rl = roofline_gemm1(head)
-    rl["traffic"] = _load_traffic(p["name"])
+    tr = _load_traffic(p["name"])
+    rl["traffic"] = None if tr is None else tr["bytes"]
+    if tr is not None:
+        rl["traffic_detail"] = {k: tr[k] for k in ("read_bytes", "write_bytes", "calibration", "source")}
     line["roofline"] = rl
     sec = []
     for name in [s for s in args.secondary.split(",") if s and s != args.workload]:
-        del_keys = None
         r = measure(name, max(5, args.steps // 2), args.warmup)
         sec.append(secondary_entry(r))
-        del r, del_keys
+        del r
         torch.cuda.empty_cache()
     line["secondary"] = sec
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(p)
+    if args.copy_calib:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(line), flush=True)
 
 

@@ -294,10 +294,11 @@ extern "C" int fmoe_align(const int32_t* topk_ids, const float* topk_weights, in
                 kMaxExperts, static_cast<long long>(M), k, E);
   if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128)
     return fail(FMOE_ERR_UNSUPPORTED, "align: block_m=%d is not supported", block_m);
-  if (M * k > (int64_t(1) << 31) - 1 || M * k / block_m + E >= (1 << 15) * 2)
+  if (M * k > (int64_t(1) << 31) - 1 || M * k / block_m + E >= (1 << 15))
     return fail(FMOE_ERR_UNSUPPORTED, "align: %lld slots is not supported", static_cast<long long>(M * k));
   const fmoe_align_out& o = *out;
-  if (!o.expt_indx || !o.expt_scal || !o.topk_indx || !o.gate_indx || !o.gate_scal ||
+  // per-slot arrays are empty (and may be null) when M == 0
+  if ((M > 0 && (!o.expt_indx || !o.expt_scal || !o.topk_indx || !o.gate_indx || !o.gate_scal)) ||
       !o.offs_raw || !o.offs_pad || !o.tile_map || !o.n_tiles)
     return fail(FMOE_ERR_INVALID, "align: a required output pointer is null");
   if (workspace_bytes < fmoe_align_workspace_bytes(M, k, E))

@@ -20,7 +20,10 @@ def quantize_fp8_block(w: torch.Tensor, block=(128, 128)):
     if R % bR or C % bC:
         raise ValueError(f"quantize_fp8_block: {R}x{C} is not a multiple of {bR}x{bC}")
     wf = w.float().view(E, R // bR, bR, C // bC, bC)
-    s = wf.abs().amax(dim=(2, 4)).clamp_min(FP8_EPS) / FP8_MAX
+    amax = wf.abs().amax(dim=(2, 4)).clamp_min(FP8_EPS)
+    # tensor / tensor: a true (correctly rounded) division on every device;
+    # torch turns "/ python_scalar" into a reciprocal multiply on the GPU
+    s = amax / torch.full_like(amax, FP8_MAX)
     q = (wf / s[:, :, None, :, None]).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
     return q.view(E, R, C), s
 
@@ -46,7 +49,7 @@ def quantize_int4_group(w: torch.Tensor, group: int = 128):
     wf = w.float().view(E, R, G, group)
     mn = wf.amin(dim=-1)
     mx = wf.amax(dim=-1)
-    sc = ((mx - mn) / 15.0).clamp_min(1e-8).to(torch.float16)
+    sc = ((mx - mn) / torch.full_like(mx, 15.0)).clamp_min(1e-8).to(torch.float16)
     scf = sc.float()
     z = torch.clamp(torch.round(-mn / scf), 0, 15)
     q = torch.clamp(torch.round(wf / scf[..., None]) + z[..., None], 0, 15).to(torch.uint8)
