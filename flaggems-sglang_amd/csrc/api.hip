@@ -29,7 +29,7 @@ int check_routing(const fmoe_routing* r, const char* who) {
     return fail(FMOE_ERR_INVALID, "%s: routing pointer is null", who);
   if (r->n_tokens < 0 || r->top_k < 1 || r->n_experts < 1 || r->max_tiles < 0)
     return fail(FMOE_ERR_INVALID, "%s: bad routing sizes", who);
-  if (r->block_m != 16 && r->block_m != 64 && r->block_m != 128)
+  if (r->block_m != 16 && r->block_m != 64 && r->block_m != 128 && r->block_m != 256)
     return fail(FMOE_ERR_UNSUPPORTED, "%s: block_m=%d is not supported", who, r->block_m);
   return FMOE_OK;
 }
@@ -50,14 +50,18 @@ GemmParams base_params(const fmoe_routing* r) {
   return p;
 }
 
-// Tile height for the fused path: 16 = decode kernels, else the prefill tile.
+// Tile height for the fused path: 16 = decode kernels, else the prefill tile,
+// from the mean slots per expert: bf16 256-row tiles (the most efficient
+// prefill tile) once experts average >= 384 slots, 128 from 96, else 64; fp8
+// tiles stop at 128 rows (LDS holds three 128-byte stages of 128x256).
 int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
   const int64_t slots = M * k;
   const int64_t active = slots < E ? slots : E;
   if (wtype == FMOE_W_INT4 || path == 2) return kDecodeBM;
-  if (path == 1) return slots >= 96 * static_cast<int64_t>(E) ? 128 : 64;
-  if (slots <= kDecodeBM * (active > 0 ? active : 1)) return kDecodeBM;
-  return slots >= 96 * static_cast<int64_t>(E) ? 128 : 64;
+  if (path != 1 && slots <= kDecodeBM * (active > 0 ? active : 1)) return kDecodeBM;
+  const int64_t mean = slots / E;
+  if (wtype == FMOE_W_BF16 && mean >= 384) return 256;
+  return mean >= 96 ? 128 : 64;
 }
 
 }  // namespace

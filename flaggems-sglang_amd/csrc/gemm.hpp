@@ -31,6 +31,7 @@ struct GemmParams {
   int64_t out_split_stride;  // elements between split partials (GEMM2)
   int n_ntiles;            // output tiles along Nout
   int splits;              // GEMM2 split-K factor (decode path)
+  int group_m;             // prefill: M-tiles per rasterization group (0 = default)
 };
 
 enum class Mode { kGemm1Silu, kGemm2 };

@@ -1,83 +1,118 @@
-// Prefill grouped GEMM: LDS-staged MFMA tiles, one expert per M-tile.
+// Prefill grouped GEMM: one expert per M-tile; MFMA tiles fed from a ring of
+// LDS stages filled by direct-to-LDS DMA.
 //
-// Workgroup = 256 threads (4 waves, 2 x 2), tile BM x BN, 128 bytes of the
-// reduction dim per pipeline stage (bf16: 64 elements, fp8: 128 = one scale
-// block), double-buffered in LDS with one barrier per stage.  Each wave owns a
-// (BM/2) x (BN/2) sub-tile computed with 16x16 MFMA blocks:
-//   bf16: v_mfma_f32_16x16x32_bf16, two per stage;
-//   fp8 : v_mfma_f32_16x16x128_f8f6f4 (OCP e4m3), one per stage, its result
-//         scaled by a_scale[row] * w_scale[block] into the fp32 accumulator.
-// Both operands are read from LDS as 32 contiguous bytes per lane (lane group
-// g = lane/16 takes bytes 32g..32g+31 of the stage); A and B use the same
-// lane -> k assignment, so the dot products are exact permutations of the
-// textbook ones.  LDS rows are padded to 144 bytes: the 16 rows read by one
-// quarter-wave then start on distinct 4-bank groups.
+// Workgroup = 8 waves (512 threads) laid out WAVES_M x WAVES_N; tile BM x BN;
+// SB bytes of the reduction dim per row per stage (bf16: SB = 64 -> 32
+// elements, one v_mfma_f32_16x16x32_bf16 step; fp8: SB = 128 -> one 128-wide
+// scale block, one v_mfma_f32_16x16x128_f8f6f4 with its result scaled by
+// a_scale[row] * w_scale[block] into the fp32 accumulator).
 //
-// GEMM1 (gate/up + SiLU): the BN weight rows of a tile are BN/2 gate rows
-// and the matching BN/2 up rows, arranged so every wave holds gate block j
-// and up block j in the same lanes; silu(gate) * up is formed in registers
-// and only the bf16 activation is written (no intermediate in HBM).
-// GEMM2: rows scaled by the routing weight, fp32 partial written per slot;
-// the top-k sum runs in fmoe_moe_sum in fixed order.
+// Measured on MI355X, which is what the structure follows:
+//  * LDS: lane-contiguous ds_read_b128 runs at ~2x the rate of any
+//    row-strided pattern.  So a stage is stored "fragment-major": for each
+//    16-row block and each 64-byte half of the row slice, a 1 KiB unit whose
+//    16-byte slot l holds chunk l/16 (of that half) of row l%16.  The MFMA
+//    fragment of lane L is then slot L of the unit: one contiguous read.
+//  * One unit is exactly one global_load_lds_dwordx4 (64 lanes x 16 B), so the
+//    DMA writes it without staging registers or ds_write instructions.
+//  * With the DMA running, operand delivery (not LDS or MFMA issue) bounds
+//    the kernel, so the tile is as large as LDS allows (256 x 256 for bf16:
+//    128 flop per byte moved) and two or three stages are kept in flight.
+// Lane group g = L/16 sees reduction bytes 16g..16g+15 of each 64-byte half in
+// both operands, so the MFMA dot products are exact permutations of the
+// textbook ones.
+//
+// The DMA is issued from inline asm (M0 = LDS destination): the compiler then
+// does not treat the LDS ring as written by an outstanding vector-memory op
+// (it would insert vmcnt(0) before every fragment read).  Completion is
+// ordered explicitly: per-wave vmcnt wait for the stage, then s_barrier
+// without a fence (later stages keep streaming across it).
+//
+// GEMM1 (gate/up + SiLU): each wave's BN/WAVES_N weight rows are half gate rows
+// and the matching up rows, so gate block j and up block j sit in the same
+// lanes; silu(gate) * up is formed in registers and only the bf16 activation
+// is written.  GEMM2: rows scaled by the routing weight, fp32 partial per
+// slot; the top-k sum runs in fmoe_moe_sum (fixed order, deterministic).
 #include "gemm.hpp"
 
 namespace fmoe {
 namespace prefill {
 
-constexpr int kThreads = 256;
-constexpr int kStageBytes = 128;  // reduction bytes per stage and row
-constexpr int kRowBytes = kStageBytes + 16;
-constexpr int kGroupM = 8;        // M-tiles per swizzle group
+constexpr int kUnit = 1024;       // one DMA wave-instruction: 64 lanes x 16 B
+constexpr int kMaxKStages = 128;  // fp8: reduction dims up to 16384
 
-template <int BM, int BN, bool FP8, Mode MODE>
-struct Tile {
-  static constexpr int WM = BM / 2, WN = BN / 2;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int BM_, int BN_, int WAVES_M_, int WAVES_N_, int SB_, int NBUF_, bool FP8_, Mode MODE_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, WAVES_M = WAVES_M_, WAVES_N = WAVES_N_, SB = SB_,
+                       NBUF = NBUF_;
+  static constexpr bool FP8 = FP8_;
+  static constexpr Mode MODE = MODE_;
+  static constexpr int NW = WAVES_M * WAVES_N, NT = NW * 64;
+  static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   static constexpr int MI = WM / 16, NI = WN / 16;
-  static constexpr int A_CHUNKS = BM * (kStageBytes / 16) / kThreads;
-  static constexpr int B_CHUNKS = BN * (kStageBytes / 16) / kThreads;
-  static constexpr int LDS_STAGE = (BM + BN) * kRowBytes;
-  static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small");
+  static constexpr int UPB = SB / 64;                       // units per 16-row block
+  static constexpr int A_UNITS = (BM / 16) * UPB, B_UNITS = (BN / 16) * UPB;
+  static constexpr int UPW = (A_UNITS + B_UNITS) / NW;      // DMA per wave per stage
+  static constexpr int A_UPW = A_UNITS / NW;
+  static constexpr int STAGE = (A_UNITS + B_UNITS) * kUnit;
+  static constexpr int SA_WAVES = FP8 ? BM / 64 : 0;        // waves that DMA a-scales
+  static_assert((A_UNITS % NW) == 0 && (B_UNITS % NW) == 0, "units per wave");
+  static_assert(!FP8 || SB == 128, "fp8 stages hold one 128-wide scale block");
   static_assert(MODE != Mode::kGemm1Silu || NI % 2 == 0, "gate/up pairing needs even NI");
+  static_assert(NBUF >= 2 && NBUF <= 4, "ring depth");
+  static_assert(NBUF * STAGE + NBUF * BM * 4 + WAVES_N * 2 * kMaxKStages * 4 <= 160 * 1024, "LDS budget");
+  static_assert(SA_WAVES <= NW, "a-scale waves");
 };
 
-__device__ __forceinline__ void mfma_step(f32x4_t& c, const i32x8_t& a, const i32x8_t& b,
-                                          bool fp8) {
-  if (fp8) {
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-  } else {
-    bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, i32x4_t{a[0], a[1], a[2], a[3]});
-    bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, i32x4_t{b[0], b[1], b[2], b[3]});
-    bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, i32x4_t{a[4], a[5], a[6], a[7]});
-    bf16x8_t b1 = __builtin_bit_cast(bf16x8_t, i32x4_t{b[4], b[5], b[6], b[7]});
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, c, 0, 0, 0);
-  }
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-__device__ __forceinline__ i32x8_t lds_frag(const uint8_t* base) {
-  i32x4_t lo = *reinterpret_cast<const i32x4_t*>(base);
-  i32x4_t hi = *reinterpret_cast<const i32x4_t*>(base + 16);
-  return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+__device__ __forceinline__ void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* l) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(l)));
+}
+// lane i's 16 (or 4) bytes land at LDS address l + 16 i (4 i)
+__device__ __forceinline__ void dma16(const uint8_t* g, uint8_t* l) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(l));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const float* g, float* l) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr(l));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "s"(m0) : "memory", "m0");
 }
 
-template <int BM, int BN, bool FP8, Mode MODE>
-__global__ __launch_bounds__(kThreads) void gemm_prefill_kernel(GemmParams p) {
-  using T = Tile<BM, BN, FP8, MODE>;
-  constexpr int WM = T::WM, WN = T::WN, MI = T::MI, NI = T::NI;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * T::LDS_STAGE];
-  __shared__ float sa_lds[FP8 ? 2 : 1][FP8 ? BM : 1];
+__device__ __forceinline__ i32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<const i32x4_t*>(p); }
 
-  const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
-  const int wm = wid / 2, wn = wid % 2;
+template <class C>
+__global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
+  constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, MI = C::MI, NI = C::NI;
+  constexpr int SB = C::SB, UPB = C::UPB, NW = C::NW, NBUF = C::NBUF;
+  constexpr bool FP8 = C::FP8;
+  constexpr Mode MODE = C::MODE;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NBUF][C::STAGE];
+  __shared__ __attribute__((aligned(256))) float sa_lds[NBUF][FP8 ? BM : 1];
+  __shared__ float sb_lds[C::WAVES_N][2][FP8 ? kMaxKStages : 1];
+
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wid / C::WAVES_N, wn = wid % C::WAVES_N;
 
   // ---- which (M-tile, N-tile): XCD-contiguous, then grouped along M
   const int n_tiles = *p.n_tiles;
   const int live = n_tiles * p.n_ntiles;
   if (static_cast<int>(blockIdx.x) >= live) return;
   const int L = xcd_remap(blockIdx.x, live);
-  const int per_group = kGroupM * p.n_ntiles;
-  const int first_m = (L / per_group) * kGroupM;
-  const int gsize = min(n_tiles - first_m, kGroupM);
+  const int per_group = p.group_m * p.n_ntiles;
+  const int first_m = (L / per_group) * p.group_m;
+  const int gsize = min(n_tiles - first_m, p.group_m);
   const int mt = first_m + (L % per_group) % gsize;
   const int nt = (L % per_group) / gsize;
 
@@ -87,85 +122,74 @@ __global__ __launch_bounds__(kThreads) void gemm_prefill_kernel(GemmParams p) {
   const int row_end = min(p.offs_raw[e + 1], row_beg + BM);
 
   const int64_t kbytes = FP8 ? p.Kred : p.Kred * 2;  // bytes per operand row
-  const int nk = static_cast<int>(kbytes / kStageBytes);
+  const int nk = static_cast<int>(kbytes / SB);
   const int ksb = static_cast<int>(p.Kred / 128);      // fp8 scale blocks per row
 
-  // ---- per-thread global source rows
-  const int c16 = tid & 7;
-  const uint8_t* a_src[T::A_CHUNKS];
-#pragma unroll
-  for (int i = 0; i < T::A_CHUNKS; ++i) {
-    int r = (tid >> 3) + i * (kThreads / 8);
+  auto a_src_row = [&](int r) -> int64_t {
     int s = row_beg + r;
     if (s >= row_end) s = row_beg;  // padding row: any valid row, result discarded
-    int64_t src = MODE == Mode::kGemm1Silu ? p.topk_indx[s] / p.top_k : s;
-    a_src[i] = p.A + src * kbytes + c16 * 16;
-  }
-  const uint8_t* b_src[T::B_CHUNKS];
+    return MODE == Mode::kGemm1Silu ? p.topk_indx[s] / p.top_k : s;
+  };
+  // ---- DMA sources: unit u = NW i + wid -> block u / UPB, half u % UPB;
+  // lane l: row l % 16 of the block, 16-byte chunk 4 half + l / 16.
   const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * kbytes;
+  const uint8_t* src[C::UPW];
+  int loff[C::UPW];
 #pragma unroll
-  for (int i = 0; i < T::B_CHUNKS; ++i) {
-    int r = (tid >> 3) + i * (kThreads / 8);
-    int64_t brow;
-    if (MODE == Mode::kGemm1Silu) {
-      int w = r / WN, within = r % WN;
-      int64_t j = static_cast<int64_t>(nt) * (BN / 2) + w * (WN / 2) + (within % (WN / 2));
-      brow = within < WN / 2 ? j : p.N_act + j;
+  for (int i = 0; i < C::UPW; ++i) {
+    const int u = NW * i + wid;
+    const int b = u / UPB, hf = u % UPB;
+    const int coff = (4 * hf + (lane >> 4)) * 16;
+    loff[i] = u * kUnit;
+    if (i < C::A_UPW) {
+      src[i] = p.A + a_src_row(b * 16 + (lane & 15)) * kbytes + coff;
     } else {
-      brow = static_cast<int64_t>(nt) * BN + r;
-      if (brow >= p.Nout) brow = p.Nout - 1;
+      const int r = (b - BM / 16) * 16 + (lane & 15);  // row of the B tile
+      int64_t brow;
+      if (MODE == Mode::kGemm1Silu) {
+        const int w = r / WN, within = r % WN;
+        const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + w * (WN / 2) + (within % (WN / 2));
+        brow = within < WN / 2 ? j : p.N_act + j;
+      } else {
+        brow = static_cast<int64_t>(nt) * BN + r;
+        if (brow >= p.Nout) brow = p.Nout - 1;
+      }
+      src[i] = Be + brow * kbytes + coff;
     }
-    b_src[i] = Be + brow * kbytes + c16 * 16;
   }
+  // fp8: waves 0 .. BM/64-1 DMA the activation scales of rows 64 wid + lane
   const float* sa_src = nullptr;
-  if (FP8 && tid < BM) {
-    int s = row_beg + tid;
-    if (s >= row_end) s = row_beg;
-    int64_t src = MODE == Mode::kGemm1Silu ? p.topk_indx[s] / p.top_k : s;
-    sa_src = p.a_scale + src * ksb;
-  }
-  // fp8 weight-scale rows for this wave (gate / up blocks, or the GEMM2 block)
-  const float* sb_src0 = nullptr;
-  const float* sb_src1 = nullptr;
+  if (FP8 && wid < C::SA_WAVES) sa_src = p.a_scale + a_src_row(64 * wid + lane) * ksb;
+  // fp8 weight scales of the whole k range, staged once in LDS
   if (FP8) {
     const int64_t nrb = p.Nout / 128;
     const float* se = p.b_scale + static_cast<int64_t>(e) * nrb * ksb;
+    const float* s0;
+    const float* s1;
     if (MODE == Mode::kGemm1Silu) {
-      int64_t j = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2);
-      sb_src0 = se + (j / 128) * ksb;
-      sb_src1 = se + ((p.N_act + j) / 128) * ksb;
+      const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2);
+      s0 = se + (j / 128) * ksb;
+      s1 = se + ((p.N_act + j) / 128) * ksb;
     } else {
       int64_t j = static_cast<int64_t>(nt) * BN + wn * WN;
       if (j >= p.Nout) j = p.Nout - 1;
-      sb_src0 = se + (j / 128) * ksb;
-      sb_src1 = sb_src0;
+      s0 = se + (j / 128) * ksb;
+      s1 = s0;
     }
+    if (wm == 0)
+      for (int kk = lane; kk < nk; kk += kWave) {
+        sb_lds[wn][0][kk] = s0[kk];
+        sb_lds[wn][1][kk] = s1[kk];
+      }
+    __syncthreads();
   }
 
-  i32x4_t ra[T::A_CHUNKS], rb[T::B_CHUNKS];
-  float rsa = 0.f;
-  auto gload = [&](int kt) {
-    const int64_t off = static_cast<int64_t>(kt) * kStageBytes;
+  auto issue = [&](int kt) {
+    uint8_t* st = lds[kt % NBUF];
+    const int64_t off = static_cast<int64_t>(kt) * SB;
 #pragma unroll
-    for (int i = 0; i < T::A_CHUNKS; ++i) ra[i] = *reinterpret_cast<const i32x4_t*>(a_src[i] + off);
-#pragma unroll
-    for (int i = 0; i < T::B_CHUNKS; ++i) rb[i] = *reinterpret_cast<const i32x4_t*>(b_src[i] + off);
-    if (FP8 && sa_src) rsa = sa_src[kt];
-  };
-  auto lstore = [&](int buf) {
-    uint8_t* As = lds + buf * T::LDS_STAGE;
-    uint8_t* Bs = As + BM * kRowBytes;
-#pragma unroll
-    for (int i = 0; i < T::A_CHUNKS; ++i) {
-      int r = (tid >> 3) + i * (kThreads / 8);
-      *reinterpret_cast<i32x4_t*>(As + r * kRowBytes + c16 * 16) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < T::B_CHUNKS; ++i) {
-      int r = (tid >> 3) + i * (kThreads / 8);
-      *reinterpret_cast<i32x4_t*>(Bs + r * kRowBytes + c16 * 16) = rb[i];
-    }
-    if (FP8 && tid < BM) sa_lds[buf][tid] = rsa;
+    for (int i = 0; i < C::UPW; ++i) dma16(src[i] + off, st + loff[i]);
+    if (FP8 && wid < C::SA_WAVES) dma4(sa_src + kt, &sa_lds[kt % NBUF][64 * wid]);
   };
 
   f32x4_t acc[MI][NI];
@@ -174,32 +198,34 @@ __global__ __launch_bounds__(kThreads) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
-
-  const int frag_off = (lane & 15) * kRowBytes + (lane >> 4) * 32;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
-    const uint8_t* As = lds + cur * T::LDS_STAGE;
-    const uint8_t* Bs = As + BM * kRowBytes;
-    i32x8_t fa[MI], fb[NI];
+  const int lane16 = lane * 16;
+  auto compute = [&](int kt) {
+    const uint8_t* st = lds[kt % NBUF];
+    const uint8_t* As = st + (wm * MI) * UPB * kUnit + lane16;
+    const uint8_t* Bs = st + (C::A_UNITS + wn * NI * UPB) * kUnit + lane16;
+    if constexpr (FP8) {
+      i32x8_t fa[MI], fb[NI];
 #pragma unroll
-    for (int i = 0; i < MI; ++i) fa[i] = lds_frag(As + (wm * WM + i * 16) * kRowBytes + frag_off);
+      for (int i = 0; i < MI; ++i) {
+        i32x4_t lo = lds16(As + (2 * i) * kUnit), hi = lds16(As + (2 * i + 1) * kUnit);
+        fa[i] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
 #pragma unroll
-    for (int j = 0; j < NI; ++j) fb[j] = lds_frag(Bs + (wn * WN + j * 16) * kRowBytes + frag_off);
-    if (FP8) {
-      const float sb0 = sb_src0[kt], sb1 = sb_src1[kt];
+      for (int j = 0; j < NI; ++j) {
+        i32x4_t lo = lds16(Bs + (2 * j) * kUnit), hi = lds16(Bs + (2 * j + 1) * kUnit);
+        fb[j] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+      const float sb0 = sb_lds[wn][0][kt], sb1 = sb_lds[wn][1][kt];
+      const float* sa_st = sa_lds[kt % NBUF];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         float sa[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sa[r] = sa_lds[cur][wm * WM + i * 16 + (lane >> 4) * 4 + r];
+        for (int r = 0; r < 4; ++r) sa[r] = sa_st[wm * WM + i * 16 + (lane >> 4) * 4 + r];
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
           f32x4_t t = {0.f, 0.f, 0.f, 0.f};
-          mfma_step(t, fa[i], fb[j], true);
+          t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa[i], fb[j], t, 0, 0, 0, 0, 0, 0);
           const float sb = (MODE == Mode::kGemm1Silu && j >= NI / 2) ? sb1 : sb0;
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[i][j][r] += t[r] * (sa[r] * sb);
@@ -207,12 +233,40 @@ __global__ __launch_bounds__(kThreads) void gemm_prefill_kernel(GemmParams p) {
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < MI; ++i)
+      for (int hf = 0; hf < UPB; ++hf) {
+        bf16x8_t fa[MI], fb[NI];
 #pragma unroll
-        for (int j = 0; j < NI; ++j) mfma_step(acc[i][j], fa[i], fb[j], false);
+        for (int i = 0; i < MI; ++i)
+          fa[i] = __builtin_bit_cast(bf16x8_t, lds16(As + (i * UPB + hf) * kUnit));
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+          fb[j] = __builtin_bit_cast(bf16x8_t, lds16(Bs + (j * UPB + hf) * kUnit));
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NI; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      }
     }
-    if (kt + 1 < nk) lstore(cur ^ 1);
-    __syncthreads();
+  };
+
+  // ring: up to NBUF-2 stages newer than kt stay in flight while kt is consumed
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s)
+    if (s < nk) issue(s);
+  constexpr int kPer = C::UPW;  // DMA instructions per stage for this wave
+  constexpr int kPerSa = C::UPW + (FP8 ? 1 : 0);
+  const bool sa_wave = FP8 && wid < C::SA_WAVES;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int newer = min(NBUF - 2, nk - 1 - kt);
+    if (sa_wave) {
+      if (newer >= 2) wait_vmcnt<2 * kPerSa>(); else if (newer == 1) wait_vmcnt<kPerSa>(); else wait_vmcnt<0>();
+    } else {
+      if (newer >= 2) wait_vmcnt<2 * kPer>(); else if (newer == 1) wait_vmcnt<kPer>(); else wait_vmcnt<0>();
+    }
+    barrier_nofence();
+    if (kt + NBUF - 1 < nk) issue(kt + NBUF - 1);
+    compute(kt);
   }
 
   // ---- epilogue.  C layout of a 16x16 block: lane holds column lane%16,
@@ -246,39 +300,48 @@ __global__ __launch_bounds__(kThreads) void gemm_prefill_kernel(GemmParams p) {
   }
 }
 
-}  // namespace prefill
-
-// Host launcher: picks the instantiation.
-int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p0, hipStream_t s) {
+template <class C>
+int launch(const GemmParams& p0, hipStream_t s) {
   GemmParams p = p0;
-  constexpr int BN = 256;
-  const int64_t ncols = mode == Mode::kGemm1Silu ? p.N_act : p.Nout;
-  const int per_tile = mode == Mode::kGemm1Silu ? BN / 2 : BN;
+  const int64_t ncols = C::MODE == Mode::kGemm1Silu ? p.N_act : p.Nout;
+  const int per_tile = C::MODE == Mode::kGemm1Silu ? C::BN / 2 : C::BN;
   p.n_ntiles = static_cast<int>((ncols + per_tile - 1) / per_tile);
+  if (p.group_m <= 0) p.group_m = 8;
   const int64_t grid = static_cast<int64_t>(p.max_tiles) * p.n_ntiles;
   if (grid <= 0) return FMOE_OK;
   if (grid > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill grid too large");
-  dim3 g(static_cast<unsigned>(grid)), b(prefill::kThreads);
-#define LAUNCH(BM_, FP8_, MODE_) \
-  prefill::gemm_prefill_kernel<BM_, BN, FP8_, MODE_><<<g, b, 0, s>>>(p)
-  const bool fp8 = wt == WType::kFp8;
-  if (bm == 128) {
-    if (mode == Mode::kGemm1Silu) {
-      if (fp8) LAUNCH(128, true, Mode::kGemm1Silu); else LAUNCH(128, false, Mode::kGemm1Silu);
-    } else {
-      if (fp8) LAUNCH(128, true, Mode::kGemm2); else LAUNCH(128, false, Mode::kGemm2);
-    }
-  } else if (bm == 64) {
-    if (mode == Mode::kGemm1Silu) {
-      if (fp8) LAUNCH(64, true, Mode::kGemm1Silu); else LAUNCH(64, false, Mode::kGemm1Silu);
-    } else {
-      if (fp8) LAUNCH(64, true, Mode::kGemm2); else LAUNCH(64, false, Mode::kGemm2);
-    }
-  } else {
-    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill: block_m=%d is not supported", bm);
-  }
-#undef LAUNCH
+  if (C::FP8 && p.Kred / 128 > kMaxKStages)
+    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill fp8: reduction dim %lld is not supported",
+                           static_cast<long long>(p.Kred));
+  gemm_prefill_kernel<C><<<dim3(static_cast<unsigned>(grid)), dim3(C::NT), 0, s>>>(p);
   return fmoe_host::check_launch("gemm_prefill");
+}
+
+}  // namespace prefill
+
+// Host launcher: picks the instantiation for the tile height.
+//   bf16: BM 256 -> 256x256, 4x2 waves, 64-byte stages, 3-deep ring
+//         BM 128 -> 128x256, 2x4 waves, 64-byte stages, 4-deep ring
+//         BM  64 ->  64x256, 1x4 waves, 64-byte stages, 4-deep ring
+//   fp8 : BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
+//         BM  64 ->  64x256, 1x8 waves, 128-byte stages, 3-deep ring
+int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s) {
+  using namespace prefill;
+  const bool fp8 = wt == WType::kFp8;
+#define L(BM, BN, WMS, WNS, SB, NB, F8)                                                      \
+  (mode == Mode::kGemm1Silu ? launch<Cfg<BM, BN, WMS, WNS, SB, NB, F8, Mode::kGemm1Silu>>(p, s) \
+                            : launch<Cfg<BM, BN, WMS, WNS, SB, NB, F8, Mode::kGemm2>>(p, s))
+  if (!fp8) {
+    if (bm == 256) return L(256, 256, 4, 2, 64, 3, false);
+    if (bm == 128) return L(128, 256, 2, 4, 64, 4, false);
+    if (bm == 64) return L(64, 256, 1, 4, 64, 4, false);
+  } else {
+    if (bm == 128) return L(128, 256, 2, 4, 128, 3, true);
+    if (bm == 64) return L(64, 256, 1, 8, 128, 3, true);
+  }
+#undef L
+  return fmoe_host::fail(FMOE_ERR_UNSUPPORTED,
+                         "prefill: block_m=%d is not supported for this weight type", bm);
 }
 
 }  // namespace fmoe
