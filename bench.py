@@ -161,7 +161,7 @@ def stage_times(p, reps=10):
         ev[0].record()
         a = F._align(p["tw"], p["ti"], E, bm, False)
         r = _lib.Routing(a.topk_indx.data_ptr(), a.gate_indx.data_ptr(), a.gate_scal.data_ptr(),
-                         a.offs_raw.data_ptr(), a.tile_map.data_ptr(), a.n_tiles.data_ptr(), M, k, E,
+                         a.offs_raw.data_ptr(), a.offs_pad.data_ptr(), a.tile_map.data_ptr(), a.n_tiles.data_ptr(), M, k, E,
                          bm, L.fmoe_max_tiles(slots, E))
         ev[1].record()
         xa, xs = p["x"], None

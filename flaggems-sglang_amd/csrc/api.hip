@@ -14,6 +14,8 @@ namespace {
 constexpr int kDecodeBM = 16;
 constexpr int kDecodeBN = 64;
 constexpr int kDecodeTargetWgs = 1024;
+constexpr int kPrefillBN = 256;
+constexpr int kPrefillTargetWgs = 6 * 256;
 
 size_t al(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -31,6 +33,8 @@ int check_routing(const fmoe_routing* r, const char* who) {
     return fail(FMOE_ERR_INVALID, "%s: bad routing sizes", who);
   if (r->block_m != 16 && r->block_m != 64 && r->block_m != 128 && r->block_m != 256)
     return fail(FMOE_ERR_UNSUPPORTED, "%s: block_m=%d is not supported", who, r->block_m);
+  if (r->block_m != 16 && !r->offs_pad)
+    return fail(FMOE_ERR_INVALID, "%s: prefill routing needs offs_pad", who);
   return FMOE_OK;
 }
 
@@ -42,9 +46,11 @@ GemmParams base_params(const fmoe_routing* r) {
   p.topk_indx = r->topk_indx;
   p.gate_scal = r->gate_scal;
   p.offs_raw = r->offs_raw;
+  p.offs_pad = r->offs_pad;
   p.tile_map = r->tile_map;
   p.n_tiles = r->n_tiles;
   p.top_k = r->top_k;
+  p.n_experts = r->n_experts;
   p.max_tiles = r->max_tiles;
   p.splits = 1;
   return p;
@@ -72,7 +78,21 @@ extern "C" int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path)
 
 extern "C" int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_routing* r, int path) {
   (void)path;
-  if (!r || !is_decode(r)) return 1;
+  if (!r) return 1;
+  if (!is_decode(r)) {
+    // Prefill GEMM2 has few output tiles (K / 256 per M-tile): split the
+    // reduction dim until the grid covers >= 6 waves of one workgroup per CU,
+    // so the last wave's tail stays small.  Partials are summed by moe_sum.
+    const int64_t slots = r->n_tokens * r->top_k;
+    const int64_t tiles = (slots + r->block_m - 1) / r->block_m;
+    const int64_t wgs = tiles * ((K + kPrefillBN - 1) / kPrefillBN);
+    const int64_t stage_elems = wtype == FMOE_W_BF16 ? 32 : 128;
+    int64_t sp = (kPrefillTargetWgs + wgs - 1) / (wgs > 0 ? wgs : 1);
+    const int64_t max_sp = N / stage_elems / 16 > 1 ? N / stage_elems / 16 : 1;  // >= 16 stages each
+    if (sp > max_sp) sp = max_sp;
+    if (sp > 4) sp = 4;
+    return static_cast<int>(sp < 1 ? 1 : sp);
+  }
   const int64_t slots = r->n_tokens * r->top_k;
   const int64_t est_tiles = slots < r->n_experts ? (slots > 0 ? slots : 1) : r->n_experts;
   const int64_t ntiles = (K + kDecodeBN - 1) / kDecodeBN;
@@ -139,8 +159,8 @@ extern "C" int fmoe_gemm2(int wtype, const void* act, const float* act_scale, co
     return fail(FMOE_ERR_UNSUPPORTED, "gemm2: int4 weights need block_m=16 routing");
   if ((path == 1 && is_decode(r)) || (path == 2 && !is_decode(r)))
     return fail(FMOE_ERR_INVALID, "gemm2: path %d does not match block_m=%d", path, r->block_m);
-  if (splits < 1 || (splits > 1 && !is_decode(r)))
-    return fail(FMOE_ERR_INVALID, "gemm2: splits=%d (split-K only on the decode path)", splits);
+  if (splits < 1 || splits > 64)
+    return fail(FMOE_ERR_INVALID, "gemm2: splits=%d out of range", splits);
   GemmParams p = base_params(r);
   p.A = static_cast<const uint8_t*>(act);
   p.a_scale = act_scale;
@@ -266,6 +286,7 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   r.gate_indx = o.gate_indx;
   r.gate_scal = o.gate_scal;
   r.offs_raw = o.offs_raw;
+  r.offs_pad = o.offs_pad;
   r.tile_map = o.tile_map;
   r.n_tiles = o.n_tiles;
   r.n_tokens = a->M;

@@ -22,16 +22,18 @@ struct GemmParams {
   const int32_t* topk_indx;
   const float* gate_scal;
   const int32_t* offs_raw;
+  const int32_t* offs_pad;   // [E+1] tile offsets per expert
   const int32_t* tile_map;
   const int32_t* n_tiles;
   int top_k;
+  int n_experts;
   int max_tiles;
   int gamma;               // multiply rows by gate_scal[slot]
   void* out;               // GEMM1: act bf16 [M*k, N]; GEMM2: y fp32 [splits][M*k, Nout]
   int64_t out_split_stride;  // elements between split partials (GEMM2)
   int n_ntiles;            // output tiles along Nout
   int splits;              // GEMM2 split-K factor (decode path)
-  int group_m;             // prefill: M-tiles per rasterization group (0 = default)
+  int group_tiles;         // prefill: concurrent tiles per rasterization window (0 = default)
 };
 
 enum class Mode { kGemm1Silu, kGemm2 };

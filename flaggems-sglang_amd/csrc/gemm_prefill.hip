@@ -40,6 +40,7 @@ namespace prefill {
 
 constexpr int kUnit = 1024;       // one DMA wave-instruction: 64 lanes x 16 B
 constexpr int kMaxKStages = 128;  // fp8: reduction dims up to 16384
+constexpr int kGroupTiles = 32;   // tiles per rasterization window (~ one XCD's CUs)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -91,6 +92,19 @@ __device__ __forceinline__ void dma4(const float* g, float* l) {
 
 __device__ __forceinline__ i32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<const i32x4_t*>(p); }
 
+// Expert e with offs_pad[e] * nn <= key < offs_pad[e + 1] * nn (offs_pad is
+// non-decreasing, offs_pad[0] = 0, key < offs_pad[E] * nn): two rounds of 64
+// parallel probes and a ballot, instead of a serial binary search.
+__device__ __forceinline__ int find_expert(const int32_t* offs_pad, int E, int key, int nn, int lane) {
+  const int S = (E + 1 + kWave - 1) / kWave;
+  const int i1 = min(lane * S, E);
+  uint64_t b = __ballot(offs_pad[i1] * nn <= key);
+  const int base = (63 - __builtin_clzll(b)) * S;
+  const int i2 = min(base + lane, E);
+  b = __ballot(lane < S && offs_pad[i2] * nn <= key);
+  return base + (63 - __builtin_clzll(b));
+}
+
 template <class C>
 __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, MI = C::MI, NI = C::NI;
@@ -105,25 +119,37 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wm = wid / C::WAVES_N, wn = wid % C::WAVES_N;
 
-  // ---- which (M-tile, N-tile): XCD-contiguous, then grouped along M
-  const int n_tiles = *p.n_tiles;
-  const int live = n_tiles * p.n_ntiles;
+  // ---- which (split, expert M-tile, N-tile).  Workgroup ids are first made
+  // XCD-contiguous; then, per expert, windows of all its T M-tiles x G N-tiles
+  // (T * G ~ group_tiles, about what one XCD runs at once) are enumerated
+  // M-fastest, so the tiles that share a weight panel run together on one XCD
+  // and the panel is fetched from HBM once.
+  const int nn = p.n_ntiles;
+  const int per_split = *p.n_tiles * nn;
+  const int live = per_split * p.splits;
   if (static_cast<int>(blockIdx.x) >= live) return;
-  const int L = xcd_remap(blockIdx.x, live);
-  const int per_group = p.group_m * p.n_ntiles;
-  const int first_m = (L / per_group) * p.group_m;
-  const int gsize = min(n_tiles - first_m, p.group_m);
-  const int mt = first_m + (L % per_group) % gsize;
-  const int nt = (L % per_group) / gsize;
-
-  const int tm = p.tile_map[mt];
-  const int e = tm & 0xffff, blk = tm >> 16;
+  int L = xcd_remap(blockIdx.x, live);
+  const int split = L / per_split;
+  L -= split * per_split;
+  const int e = find_expert(p.offs_pad, p.n_experts, L, nn, lane);
+  const int t0 = p.offs_pad[e];
+  const int T = p.offs_pad[e + 1] - t0;
+  const int local = L - t0 * nn;
+  const int G = max(1, p.group_tiles / T);
+  const int grp = local / (T * G);
+  const int rr = local - grp * T * G;
+  const int blk = rr % T;
+  const int nt = grp * G + rr / T;
   const int row_beg = p.offs_raw[e] + blk * BM;
   const int row_end = min(p.offs_raw[e + 1], row_beg + BM);
 
   const int64_t kbytes = FP8 ? p.Kred : p.Kred * 2;  // bytes per operand row
-  const int nk = static_cast<int>(kbytes / SB);
+  const int nk_all = static_cast<int>(kbytes / SB);
   const int ksb = static_cast<int>(p.Kred / 128);      // fp8 scale blocks per row
+  // split-K: this workgroup reduces stages [k0, k0 + nk)
+  const int per_k = (nk_all + p.splits - 1) / p.splits;
+  const int k0 = min(nk_all, split * per_k);
+  const int nk = min(nk_all, k0 + per_k) - k0;
 
   auto a_src_row = [&](int r) -> int64_t {
     int s = row_beg + r;
@@ -142,7 +168,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     const int coff = (4 * hf + (lane >> 4)) * 16;
     loff[i] = u * kUnit;
     if (i < C::A_UPW) {
-      src[i] = p.A + a_src_row(b * 16 + (lane & 15)) * kbytes + coff;
+      src[i] = p.A + a_src_row(b * 16 + (lane & 15)) * kbytes + static_cast<int64_t>(k0) * SB + coff;
     } else {
       const int r = (b - BM / 16) * 16 + (lane & 15);  // row of the B tile
       int64_t brow;
@@ -154,12 +180,12 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
         brow = static_cast<int64_t>(nt) * BN + r;
         if (brow >= p.Nout) brow = p.Nout - 1;
       }
-      src[i] = Be + brow * kbytes + coff;
+      src[i] = Be + brow * kbytes + static_cast<int64_t>(k0) * SB + coff;
     }
   }
   // fp8: waves 0 .. BM/64-1 DMA the activation scales of rows 64 wid + lane
   const float* sa_src = nullptr;
-  if (FP8 && wid < C::SA_WAVES) sa_src = p.a_scale + a_src_row(64 * wid + lane) * ksb;
+  if (FP8 && wid < C::SA_WAVES) sa_src = p.a_scale + a_src_row(64 * wid + lane) * ksb + k0;
   // fp8 weight scales of the whole k range, staged once in LDS
   if (FP8) {
     const int64_t nrb = p.Nout / 128;
@@ -178,8 +204,8 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     }
     if (wm == 0)
       for (int kk = lane; kk < nk; kk += kWave) {
-        sb_lds[wn][0][kk] = s0[kk];
-        sb_lds[wn][1][kk] = s1[kk];
+        sb_lds[wn][0][kk] = s0[k0 + kk];
+        sb_lds[wn][1][kk] = s1[k0 + kk];
       }
     __syncthreads();
   }
@@ -289,7 +315,8 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
           act[col] = f32_to_bf16(silu_mul(gv, uv));
         }
       } else {
-        float* y = static_cast<float*>(p.out) + static_cast<int64_t>(s) * p.Nout;
+        float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
+                   static_cast<int64_t>(s) * p.Nout;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
           const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + col16;
@@ -306,8 +333,9 @@ int launch(const GemmParams& p0, hipStream_t s) {
   const int64_t ncols = C::MODE == Mode::kGemm1Silu ? p.N_act : p.Nout;
   const int per_tile = C::MODE == Mode::kGemm1Silu ? C::BN / 2 : C::BN;
   p.n_ntiles = static_cast<int>((ncols + per_tile - 1) / per_tile);
-  if (p.group_m <= 0) p.group_m = 8;
-  const int64_t grid = static_cast<int64_t>(p.max_tiles) * p.n_ntiles;
+  if (p.group_tiles <= 0) p.group_tiles = kGroupTiles;
+  if (p.splits < 1) p.splits = 1;
+  const int64_t grid = static_cast<int64_t>(p.max_tiles) * p.n_ntiles * p.splits;
   if (grid <= 0) return FMOE_OK;
   if (grid > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill grid too large");
   if (C::FP8 && p.Kred / 128 > kMaxKStages)

@@ -39,7 +39,7 @@ class AlignOut(ctypes.Structure):
 class Routing(ctypes.Structure):
     _fields_ = [
         ("topk_indx", vp), ("gate_indx", vp), ("gate_scal", vp), ("offs_raw", vp),
-        ("tile_map", vp), ("n_tiles", vp), ("n_tokens", ctypes.c_int64), ("top_k", ctypes.c_int32),
+        ("offs_pad", vp), ("tile_map", vp), ("n_tiles", vp), ("n_tokens", ctypes.c_int64), ("top_k", ctypes.c_int32),
         ("n_experts", ctypes.c_int32), ("block_m", ctypes.c_int32), ("max_tiles", ctypes.c_int32),
     ]
 

@@ -192,12 +192,12 @@ def _standard_topk_to_triton_kernels(topk_weights, topk_ids, n_expts_tot, block_
 
 
 def _expt_data_for(routing_data: RoutingData, n_slots: int, block_m: int):
-    """(offs_raw, tile_map, n_tiles) for ``block_m``: reuse the routing's own
-    ExptData when it has this tile height, else derive it from the histogram
-    (compute_expt_data_torch, ops/fused_moe.py:124)."""
+    """(offs_raw, offs_pad, tile_map, n_tiles) for ``block_m``: reuse the
+    routing's own ExptData when it has this tile height, else derive it from
+    the histogram (compute_expt_data_torch, ops/fused_moe.py:124)."""
     ed = routing_data.expt_data
     if ed is not None and block_m in getattr(ed, "block_pid_map", {}) and block_m in getattr(ed, "n_tiles", {}):
-        return ed.token_offs_raw, ed.block_pid_map[block_m], ed.n_tiles[block_m]
+        return ed.token_offs_raw, ed.token_offs_pad[block_m], ed.block_pid_map[block_m], ed.n_tiles[block_m]
     L = lib()
     E = routing_data.n_expts_tot
     hist = routing_data.expt_hist.to(torch.int32).contiguous()
@@ -214,7 +214,7 @@ def _expt_data_for(routing_data: RoutingData, n_slots: int, block_m: int):
         ed.block_pid_map[block_m] = tile_map
         if isinstance(getattr(ed, "n_tiles", None), dict):
             ed.n_tiles[block_m] = n_tiles
-    return offs_raw, tile_map, n_tiles
+    return offs_raw, offs_pad, tile_map, n_tiles
 
 
 # ---------------------------------------------------------------------------
@@ -266,8 +266,8 @@ def _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w
 
 
 def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens, top_k,
-                n_experts, topk_indx, gate_indx, gate_scal, offs_raw, tile_map, n_tiles, block_m,
-                apply_router_weight_on_input, scale, combine=True):
+                n_experts, topk_indx, gate_indx, gate_scal, offs_raw, offs_pad, tile_map, n_tiles,
+                block_m, apply_router_weight_on_input, scale, combine=True):
     """GEMM1+SiLU -> GEMM2 -> top-k sum on prepared routing, SGLang layouts
     ``w13 [E, 2N, K]``, ``w2 [E, K, N]``."""
     L = lib()
@@ -275,8 +275,8 @@ def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens,
     N = w2.shape[2] * (2 if wtype == W_INT4 else 1)
     dev = x.device
     st = stream_of(x)
-    r = _lib.Routing(ptr(topk_indx), ptr(gate_indx), ptr(gate_scal), ptr(offs_raw), ptr(tile_map),
-                     ptr(n_tiles), n_tokens, top_k, n_experts, block_m,
+    r = _lib.Routing(ptr(topk_indx), ptr(gate_indx), ptr(gate_scal), ptr(offs_raw), ptr(offs_pad),
+                     ptr(tile_map), ptr(n_tiles), n_tokens, top_k, n_experts, block_m,
                      L.fmoe_max_tiles(n_tokens * top_k, n_experts))
     slots = n_tokens * top_k
     xa, xs = x, None
@@ -373,13 +373,13 @@ def triton_kernel_fused_experts(
     s13 = None if w1_scale is None else _as_sglang_layout(w1_scale)
     s2 = None if w2_scale is None else _as_sglang_layout(w2_scale)
     bm = lib().fmoe_choose_block_m(wtype, M, k, E, 0)
-    offs_raw, tile_map, n_tiles = _expt_data_for(routing_data, M * k, bm)
+    offs_raw, offs_pad, tile_map, n_tiles = _expt_data_for(routing_data, M * k, bm)
     topk_indx = gather_indx.src_indx.to(torch.int32).contiguous()
     gate_indx = gather_indx.dst_indx.to(torch.int32).contiguous()
     gate_scal = routing_data.gate_scal.float().contiguous()
     return _run_stages(x, w13, w2t, wtype, s13, s2, None, None, M, k, E, topk_indx, gate_indx,
-                       gate_scal, offs_raw, tile_map, n_tiles, bm, apply_router_weight_on_input,
-                       1.0, combine=scatter_indx is not None)
+                       gate_scal, offs_raw, offs_pad, tile_map, n_tiles, bm,
+                       apply_router_weight_on_input, 1.0, combine=scatter_indx is not None)
 
 
 def triton_kernel_fused_experts_with_bias(*args, **kwargs):
@@ -452,8 +452,8 @@ def fused_experts(
     if no_combine:
         a = _align(topk_weights, topk_ids, E, lib().fmoe_choose_block_m(wtype, M, k, E, path), False)
         return _run_stages(x, w1, w2, wtype, w1_scale, w2_scale, w1_zp, w2_zp, M, k, E,
-                           a.topk_indx, a.gate_indx, a.gate_scal, a.offs_raw, a.tile_map, a.n_tiles,
-                           a.block_m, apply_router_weight_on_input, 1.0, combine=False)
+                           a.topk_indx, a.gate_indx, a.gate_scal, a.offs_raw, a.offs_pad, a.tile_map,
+                           a.n_tiles, a.block_m, apply_router_weight_on_input, 1.0, combine=False)
     ids = _ids_i32(topk_ids)
     tw = topk_weights.float().contiguous()
     out = torch.empty(M, K, dtype=torch.bfloat16, device=x.device)

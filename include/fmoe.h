@@ -148,6 +148,7 @@ typedef struct fmoe_routing {
   const int32_t* gate_indx;
   const float* gate_scal;
   const int32_t* offs_raw;
+  const int32_t* offs_pad; /* [E+1] tile offsets (prefill rasterization) */
   const int32_t* tile_map;
   const int32_t* n_tiles;
   int64_t n_tokens;
@@ -172,7 +173,8 @@ int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const void* w13,
  * sum (ops/fused_moe.py:208-215): y[split][s, :] = act[s] @ w2[e]^T
  * [* gate_scal[s] when apply_gamma], fp32, sorted-slot order.  `splits`
  * partial sums over the reduction dim N are written to y[0..splits-1]
- * (fmoe_gemm2_splits() gives the count the library picks). */
+ * (fmoe_gemm2_splits() gives the count the library picks; every plane is
+ * written, so y needs no clearing). */
 int fmoe_gemm2(int wtype, const void* act, const float* act_scale, const void* w2,
                const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
                const fmoe_routing* r, int apply_gamma, float* y, int splits, int path,
