@@ -87,6 +87,28 @@ __device__ int block_exclusive_scan(int v, int* lds_tmp, int* total) {
   return wbase + x - v;
 }
 
+// Tile map (ExptData.block_pid_map) and SGLang expert_ids from the padded
+// tile offsets in LDS: tile tt belongs to the last expert whose offset <= tt.
+__device__ void write_tile_map(const AlignParams& p, const int* offs_pad_lds, int ttot) {
+  const int tid = threadIdx.x;
+  const int64_t nblk_cap = p.o.expert_ids ? p.sorted_cap / p.bm + 1 : 0;
+  const int64_t lim = p.max_tiles > nblk_cap ? p.max_tiles : nblk_cap;
+  for (int64_t tt = tid; tt < lim; tt += kAlignThreads) {
+    int val = -1, ex = -1;
+    if (tt < ttot) {
+      int lo = 0, hi = p.E;  // offs_pad_lds[lo] <= tt < offs_pad_lds[hi]
+      while (hi - lo > 1) {
+        int mid = (lo + hi) >> 1;
+        if (offs_pad_lds[mid] <= tt) lo = mid; else hi = mid;
+      }
+      ex = lo;
+      val = (static_cast<int>(tt - offs_pad_lds[lo]) << 16) | lo;
+    }
+    if (tt < p.max_tiles) p.o.tile_map[tt] = val;
+    if (tt < nblk_cap) p.o.expert_ids[tt] = ex;
+  }
+}
+
 // ---- phase 2: prefix over chunks and experts, ExptData, SGLang block ids.
 // hist_in != nullptr: histogram given directly (fmoe_expt_data); no chunks.
 __device__ void phase_scan(const AlignParams& p, const int32_t* hist_in, int* offs_pad_lds,
@@ -139,23 +161,7 @@ __device__ void phase_scan(const AlignParams& p, const int32_t* hist_in, int* of
     if (p.o.num_tokens_post_padded) p.o.num_tokens_post_padded[0] = ttot * p.bm;
   }
   __syncthreads();
-  // tile map: tile tt belongs to the last expert whose padded offset <= tt
-  const int64_t nblk_cap = p.o.expert_ids ? p.sorted_cap / p.bm + 1 : 0;
-  const int64_t lim = p.max_tiles > nblk_cap ? p.max_tiles : nblk_cap;
-  for (int64_t tt = tid; tt < lim; tt += kAlignThreads) {
-    int val = -1, ex = -1;
-    if (tt < ttot) {
-      int lo = 0, hi = p.E;  // offs_pad_lds[lo] <= tt < offs_pad_lds[hi]
-      while (hi - lo > 1) {
-        int mid = (lo + hi) >> 1;
-        if (offs_pad_lds[mid] <= tt) lo = mid; else hi = mid;
-      }
-      ex = lo;
-      val = (static_cast<int>(tt - offs_pad_lds[lo]) << 16) | lo;
-    }
-    if (tt < p.max_tiles) p.o.tile_map[tt] = val;
-    if (tt < nblk_cap) p.o.expert_ids[tt] = ex;
-  }
+  write_tile_map(p, offs_pad_lds, ttot);
 }
 
 // ---- phase 3: stable scatter of one chunk
@@ -258,6 +264,135 @@ __global__ __launch_bounds__(kAlignThreads) void align_small_kernel(AlignParams 
   phase_scatter(p, 0, run, wcnt, base, padshift);
 }
 
+
+// Small batches (M*k <= kTinySlots): the three phases in one workgroup with
+// every intermediate in LDS (no global round trips between phases).  Same
+// outputs, bit for bit, as the chunked path: ranks by counting within a row,
+// stable ballot ranks within an expert.
+constexpr int kTinySlots = 1024;
+
+__global__ __launch_bounds__(kAlignThreads) void align_tiny_kernel(AlignParams p) {
+  __shared__ int s_e[kTinySlots];
+  __shared__ int s_col[kTinySlots];
+  __shared__ int s_id[kTinySlots];
+  __shared__ float s_w[kTinySlots];
+  __shared__ int hist[kMaxExperts];
+  __shared__ int offs[kMaxExperts + 1];
+  __shared__ int offs_pad[kMaxExperts + 1];
+  __shared__ int wcnt[kAlignThreads / kWave][kMaxExperts];
+  __shared__ int run[kMaxExperts];
+  __shared__ int tmp[kAlignThreads / kWave];
+  const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
+  const int n = static_cast<int>(p.M * p.k);
+  fill_sentinel(p, tid, kAlignThreads);
+  for (int e = tid; e < p.E; e += kAlignThreads) {
+    hist[e] = 0;
+    run[e] = 0;
+    for (int w = 0; w < kAlignThreads / kWave; ++w) wcnt[w][e] = 0;
+  }
+  for (int f = tid; f < n; f += kAlignThreads) {  // coalesced, independent loads
+    s_id[f] = p.ids[f];
+    s_w[f] = p.w[f];
+  }
+  __syncthreads();
+  // rows: per-token counting sort of its k ids
+  for (int t = tid; t < p.M; t += kAlignThreads) {
+    const int* row = s_id + t * p.k;
+    const float* wr = s_w + t * p.k;
+    for (int j = 0; j < p.k; ++j) {
+      const int idj = row[j];
+      int rank = 0;
+      for (int i = 0; i < p.k; ++i) {
+        const int idi = row[i];
+        rank += (idi < idj) || (idi == idj && i < j);
+      }
+      const int f = t * p.k + rank;
+      s_e[f] = idj;
+      s_col[f] = j;
+      p.o.expt_indx[f] = idj;
+      p.o.expt_scal[f] = wr[j];
+      if (idj >= 0 && idj < p.E) atomicAdd(&hist[idj], 1);
+    }
+  }
+  __syncthreads();
+  // scan over experts (4 per thread, E <= 1024)
+  constexpr int PER = kMaxExperts / kAlignThreads;
+  int hv[PER], tv[PER], hsum = 0, tsum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid * PER + i;
+    hv[i] = e < p.E ? hist[e] : 0;
+    tv[i] = (hv[i] + p.bm - 1) / p.bm;
+    hsum += hv[i];
+    tsum += tv[i];
+  }
+  int htot, ttot;
+  int hb = block_exclusive_scan(hsum, tmp, &htot);
+  int tb = block_exclusive_scan(tsum, tmp, &ttot);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid * PER + i;
+    if (e < p.E) {
+      offs[e] = hb;
+      offs_pad[e] = tb;
+      if (p.o.hist) p.o.hist[e] = hv[i];
+      p.o.offs_raw[e] = hb;
+      p.o.offs_pad[e] = tb;
+    }
+    hb += hv[i];
+    tb += tv[i];
+  }
+  if (tid == 0) {
+    offs[p.E] = htot;
+    offs_pad[p.E] = ttot;
+    p.o.offs_raw[p.E] = htot;
+    p.o.offs_pad[p.E] = ttot;
+    p.o.n_tiles[0] = ttot;
+    if (p.o.num_tokens_post_padded) p.o.num_tokens_post_padded[0] = ttot * p.bm;
+  }
+  __syncthreads();
+  write_tile_map(p, offs_pad, ttot);
+  // stable scatter (ballot ranks within each wave, wave counts through LDS)
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (int f0 = 0; f0 < n; f0 += kAlignThreads) {
+    const int f = f0 + tid;
+    int e = p.E;
+    if (f < n) {
+      const int v = s_e[f];
+      if (v >= 0 && v < p.E) e = v;
+      else p.o.gate_indx[f] = -1;
+    }
+    uint64_t m = ~0ull;
+#pragma unroll
+    for (int b = 0; b < 11; ++b) {
+      const int bit = (e >> b) & 1;
+      const uint64_t v = __ballot(bit);
+      m &= bit ? v : ~v;
+    }
+    const int r = __popcll(m & lt);
+    const int cnt = __popcll(m);
+    const bool live = e < p.E;
+    const bool leader = live && r == cnt - 1;
+    if (leader) wcnt[wid][e] = cnt;
+    __syncthreads();
+    if (live) {
+      int before = run[e];
+      for (int w = 0; w < wid; ++w) before += wcnt[w][e];
+      const int pos = offs[e] + before + r;
+      p.o.topk_indx[pos] = f;
+      p.o.gate_indx[f] = pos;
+      p.o.gate_scal[pos] = p.o.expt_scal[f];
+      if (p.o.sorted_token_ids)
+        p.o.sorted_token_ids[pos + offs_pad[e] * p.bm - offs[e]] = (f / p.k) * p.k + s_col[f];
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&run[e], cnt);
+      wcnt[wid][e] = 0;
+    }
+    __syncthreads();
+  }
+}
 }  // namespace fmoe
 
 using namespace fmoe;
@@ -323,8 +458,9 @@ extern "C" int fmoe_align(const int32_t* topk_ids, const float* topk_weights, in
   p.sort_col = reinterpret_cast<int32_t*>(ws + 2 * align_up(sizeof(int32_t) * C * E));
   p.o = o;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (C <= 1) {
-    if (C == 0) p.n_chunks = 1;  // M == 0: rows phase writes nothing; scan yields zeros
+  if (M * k <= kTinySlots) {
+    align_tiny_kernel<<<1, kAlignThreads, 0, s>>>(p);
+  } else if (C <= 1) {
     align_small_kernel<<<1, kAlignThreads, 0, s>>>(p);
   } else {
     align_rows_kernel<<<static_cast<unsigned>(C), kAlignThreads, 0, s>>>(p);

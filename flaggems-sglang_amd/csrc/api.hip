@@ -116,8 +116,12 @@ extern "C" int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const 
     return fail(FMOE_ERR_UNSUPPORTED, "gemm1: K=%lld N=%lld must be multiples of 128",
                 static_cast<long long>(K), static_cast<long long>(N));
   if (!x || !w13 || !act) return fail(FMOE_ERR_INVALID, "gemm1: null pointer");
-  if (wtype == FMOE_W_FP8 && (!x_scale || !w13_scale))
-    return fail(FMOE_ERR_INVALID, "gemm1: fp8 needs x_scale and w13_scale");
+  if (wtype == FMOE_W_FP8 && !w13_scale)
+    return fail(FMOE_ERR_INVALID, "gemm1: fp8 needs w13_scale");
+  if (wtype == FMOE_W_FP8 && !is_decode(r) && !x_scale)
+    return fail(FMOE_ERR_INVALID, "gemm1: fp8 prefill needs pre-quantized x with x_scale");
+  if (wtype == FMOE_W_FP8 && is_decode(r) && x_scale)
+    return fail(FMOE_ERR_INVALID, "gemm1: fp8 decode takes bf16 x (quantized in-kernel); x_scale must be null");
   if (wtype == FMOE_W_INT4 && (!w13_scale || !w13_zero))
     return fail(FMOE_ERR_INVALID, "gemm1: int4 needs w13_scale and w13_zero");
   if (wtype == FMOE_W_INT4 && !is_decode(r))
@@ -151,8 +155,12 @@ extern "C" int fmoe_gemm2(int wtype, const void* act, const float* act_scale, co
     return fail(FMOE_ERR_UNSUPPORTED, "gemm2: K=%lld N=%lld must be multiples of 128",
                 static_cast<long long>(K), static_cast<long long>(N));
   if (!act || !w2 || !y) return fail(FMOE_ERR_INVALID, "gemm2: null pointer");
-  if (wtype == FMOE_W_FP8 && (!act_scale || !w2_scale))
-    return fail(FMOE_ERR_INVALID, "gemm2: fp8 needs act_scale and w2_scale");
+  if (wtype == FMOE_W_FP8 && !w2_scale)
+    return fail(FMOE_ERR_INVALID, "gemm2: fp8 needs w2_scale");
+  if (wtype == FMOE_W_FP8 && !is_decode(r) && !act_scale)
+    return fail(FMOE_ERR_INVALID, "gemm2: fp8 prefill needs pre-quantized act with act_scale");
+  if (wtype == FMOE_W_FP8 && is_decode(r) && act_scale)
+    return fail(FMOE_ERR_INVALID, "gemm2: fp8 decode takes bf16 act (quantized in-kernel); act_scale must be null");
   if (wtype == FMOE_W_INT4 && (!w2_scale || !w2_zero))
     return fail(FMOE_ERR_INVALID, "gemm2: int4 needs w2_scale and w2_zero");
   if (wtype == FMOE_W_INT4 && !is_decode(r))
@@ -235,7 +243,7 @@ FusedLayout layout(const fmoe_fused_args* a) {
   L.offs_pad = take(4 * (a->E + 1));
   L.tile_map = take(4 * L.max_tiles);
   L.n_tiles = take(4);
-  const bool fp8 = a->wtype == FMOE_W_FP8;
+  const bool fp8 = a->wtype == FMOE_W_FP8 && L.bm != kDecodeBM;
   L.xq = take(fp8 ? a->M * a->K : 0);
   L.xs = take(fp8 ? 4 * a->M * (a->K / 128) : 0);
   L.act = take(2 * slots * a->N);
@@ -295,7 +303,9 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   r.block_m = L.bm;
   r.max_tiles = static_cast<int32_t>(L.max_tiles);
 
-  const bool fp8 = a->wtype == FMOE_W_FP8;
+  // fp8 prefill quantizes activations in separate passes; the decode kernels
+  // quantize their bf16 rows in registers
+  const bool fp8 = a->wtype == FMOE_W_FP8 && L.bm != kDecodeBM;
   const void* x = a->x;
   const float* xs = nullptr;
   if (fp8) {

@@ -3,26 +3,33 @@
 // For small token counts every expert tile holds <= 16 slots, so the work is
 // bound by reading each touched expert's weights once.  A workgroup (4
 // waves) owns 16 slots x 64 weight rows and splits the reduction dim between
-// its waves by interleaved 128-byte stages (wave w takes stages w, w+4, ...),
-// so at any moment the four waves read adjacent 128-byte pieces of the same
-// 64 rows; lane group g = lane/16 reads bytes 32g..32g+31 (int4: 16g..16g+15)
-// of row lane%16 of each 16-row block.  No LDS staging; the per-wave partial
-// accumulators are summed through LDS once at the end.  GEMM2 may further
-// split the reduction across workgroups (`splits`); the partials land in
-// separate y planes that fmoe_moe_sum adds in fixed order.
+// its waves by interleaved stages (wave w takes stages w, w+4, ...), so at any
+// moment the four waves read adjacent pieces of the same 64 rows; lane group
+// g = lane/16 reads its part of row lane%16 of each 16-row block.  The fp8
+// GEMM1 variant keeps two stages of loads in flight per wave (its in-register
+// activation quantization is long enough to hide a second stage behind); the
+// others issue one stage at a time, which keeps VGPR use and therefore
+// occupancy higher -- measured faster for bf16 and int4.  No LDS staging;
+// the per-wave partial accumulators are summed through LDS once at the end.
+// GEMM2 may further split the reduction across workgroups (`splits`); the
+// partials land in separate y planes that fmoe_moe_sum adds in fixed order.
 //
-// Weight formats:
-//   bf16: 16 elements per lane per stage -> two v_mfma_f32_16x16x32_bf16.
-//   fp8 : 32 elements per lane per stage -> one v_mfma_f32_16x16x128_f8f6f4,
-//         scaled by a_scale * w_scale per 128-wide block.
-//   int4: 32 nibbles per lane per stage (one 128-wide quant group per stage).
-//         A nibble q becomes the bf16 number 128 + q by OR-ing 0x4300 into
-//         its 16-bit lane (exact: bf16 spacing at 128 is 1), so the MFMA
-//         computes sum((128 + q) x); with xs = sum(x) over the group (an MFMA
-//         against a ones vector) the dequantized product is
+// Weight formats (one stage = one 128-byte slice of a weight row, int4: 64):
+//   bf16: 16 elements per lane -> two v_mfma_f32_16x16x32_bf16.
+//   fp8 : 32 elements per lane -> one v_mfma_f32_16x16x128_f8f6f4, scaled by
+//         a_scale * w_scale per 128-wide block.  The activation side arrives as
+//         bf16 and is quantized here, per row and 128-group, to OCP e4m3 with
+//         scale = max(amax, 1e-10) / 448 (amax reduced over the 4 lane groups
+//         holding the row, hardware RNE conversion) -- no separate quant pass.
+//   int4: 32 nibbles per lane (one 128-wide quant group per stage).  A nibble
+//         q becomes the bf16 number 128 + q by OR-ing 0x4300 into its 16-bit
+//         lane (exact: bf16 spacing at 128 is 1), so the MFMA computes
+//         sum((128 + q) x); with xs = sum(x) over the group (an MFMA against a
+//         ones vector) the dequantized product is
 //         scale * (sum((128+q) x) - (128 + zero) * xs).
 //         The nibble pairs come out as k = (j, j+4) of each 8-nibble dword;
 //         the activations are permuted the same way with v_perm_b32.
+
 #include "gemm.hpp"
 
 namespace fmoe {
@@ -44,7 +51,31 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(int a, int b, int c, int d) {
   return __builtin_bit_cast(bf16x8_t, i32x4_t{a, b, c, d});
 }
 
-template <WType WT, Mode MODE>
+// Per-stage operand registers of one wave.
+template <WType WT>
+struct Stage;
+template <>
+struct Stage<WType::kBf16> {
+  i32x8_t a;      // 16 bf16 of the activation row
+  i32x8_t b[NI];  // 16 bf16 of each weight row
+};
+template <>
+struct Stage<WType::kFp8> {
+  i32x4_t a[4];   // 32 bf16 of the activation row (quantized in registers)
+  i32x8_t b[NI];  // 32 fp8 of each weight row
+};
+template <>
+struct Stage<WType::kInt4> {
+  i32x4_t a[4];   // 32 bf16 of the activation row
+  i32x4_t b[NI];  // 32 uint4 of each weight row
+};
+
+// Stages in flight per wave (see the file comment).
+constexpr int pipe_depth(WType wt, Mode mode) {
+  return wt == WType::kFp8 && mode == Mode::kGemm1Silu ? 2 : 1;
+}
+
+template <WType WT, Mode MODE, int PIPE>
 __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
   __shared__ f32x4_t red[kWaves][NI][kWave];
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
@@ -58,21 +89,21 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
   const int row_beg = p.offs_raw[e] + blk * BM;
   const int row_end = min(p.offs_raw[e + 1], row_beg + BM);
 
-  // A rows: row lane%16 of the tile
+  constexpr bool kFp8 = WT == WType::kFp8;
+  constexpr bool kInt4 = WT == WType::kInt4;
+  // A rows: row lane%16 of the tile (bf16 for every format)
   int s_a = row_beg + (lane & 15);
   if (s_a >= row_end) s_a = row_beg;
   const int64_t a_row = MODE == Mode::kGemm1Silu ? p.topk_indx[s_a] / p.top_k : s_a;
-  constexpr bool kFp8 = WT == WType::kFp8;
-  constexpr bool kInt4 = WT == WType::kInt4;
-  const int64_t a_bytes = kFp8 ? p.Kred : p.Kred * 2;
-  const uint8_t* a_ptr = p.A + a_row * a_bytes;
-  // stage geometry: bytes of one weight row per stage and reduction elements
-  constexpr int kWStage = kInt4 ? 64 : 128;
+  const uint8_t* a_ptr = p.A + a_row * p.Kred * 2;
+  // stage geometry
+  constexpr int kWStage = kInt4 ? 64 : 128;          // weight bytes per row per stage
+  constexpr int kElems = kInt4 ? 128 : (kFp8 ? 128 : 64);  // reduction elements per stage
   const int64_t w_bytes = kInt4 ? p.Kred / 2 : (kFp8 ? p.Kred : p.Kred * 2);
   const int nk = static_cast<int>(w_bytes / kWStage);
-  constexpr int kElems = kInt4 ? 128 : (kFp8 ? 128 : 64);  // reduction elements per stage
+  const int lane_off_w = (lane >> 4) * (kInt4 ? 16 : 32);
+  const int lane_off_a = (lane >> 4) * (WT == WType::kBf16 ? 32 : 64);  // bf16 activations
 
-  // weight rows of the 4 blocks for this lane
   const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * w_bytes;
   int64_t wrow[NI];
 #pragma unroll
@@ -88,90 +119,109 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
     wrow[j] = r;
   }
   const uint8_t* w_ptr[NI];
-  const int lane_off_w = (lane >> 4) * (kInt4 ? 16 : 32);
 #pragma unroll
   for (int j = 0; j < NI; ++j) w_ptr[j] = Be + wrow[j] * w_bytes + lane_off_w;
-  const int lane_off_a = (lane >> 4) * (kInt4 ? 64 : 32);
 
-  // fp8 scales
+  // fp8 weight-scale rows (16-row blocks never straddle a 128-row block)
   const int ksb = static_cast<int>(p.Kred / 128);
-  const float* sa_ptr[4] = {nullptr, nullptr, nullptr, nullptr};
   const float* sb_ptr[NI] = {};
   if (kFp8) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      int s = row_beg + (lane >> 4) * 4 + r;
-      if (s >= row_end) s = row_beg;
-      int64_t src = MODE == Mode::kGemm1Silu ? p.topk_indx[s] / p.top_k : s;
-      sa_ptr[r] = p.a_scale + src * ksb;
-    }
     const float* se = p.b_scale + static_cast<int64_t>(e) * (p.Nout / 128) * ksb;
 #pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      // block of the block's first row (16-row blocks never straddle 128)
-      int64_t r0 = wrow[j] - (lane & 15);
-      sb_ptr[j] = se + (r0 / 128) * ksb;
-    }
+    for (int j = 0; j < NI; ++j) sb_ptr[j] = se + ((wrow[j] - (lane & 15)) / 128) * ksb;
   }
 
   f32x4_t acc[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // split-K range over stages
-  const int per_split = (nk + p.splits - 1) / p.splits;
-  const int k_beg = split * per_split;
-  const int k_end = min(nk, k_beg + per_split);
-
-  for (int kt = k_beg + wid; kt < k_end; kt += kWaves) {
+  auto load = [&](int kt, Stage<WT>& S) {
     const int64_t woff = static_cast<int64_t>(kt) * kWStage;
-    const int64_t aoff = static_cast<int64_t>(kt) * kElems * (kFp8 ? 1 : 2);
+    const uint8_t* ap = a_ptr + static_cast<int64_t>(kt) * kElems * 2 + lane_off_a;
     if constexpr (WT == WType::kBf16) {
-      i32x8_t a = gload32(a_ptr + aoff + lane_off_a);
-      i32x8_t b[NI];
+      S.a = gload32(ap);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) b[j] = gload32(w_ptr[j] + woff);
-      bf16x8_t a0 = as_bf16x8(a[0], a[1], a[2], a[3]), a1 = as_bf16x8(a[4], a[5], a[6], a[7]);
+      for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
+    } else if constexpr (WT == WType::kFp8) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+    }
+  };
+
+  auto consume = [&](int kt, const Stage<WT>& S) {
+    if constexpr (WT == WType::kBf16) {
+      const bf16x8_t a0 = as_bf16x8(S.a[0], S.a[1], S.a[2], S.a[3]);
+      const bf16x8_t a1 = as_bf16x8(S.a[4], S.a[5], S.a[6], S.a[7]);
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            a0, as_bf16x8(b[j][0], b[j][1], b[j][2], b[j][3]), acc[j], 0, 0, 0);
+            a0, as_bf16x8(S.b[j][0], S.b[j][1], S.b[j][2], S.b[j][3]), acc[j], 0, 0, 0);
         acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            a1, as_bf16x8(b[j][4], b[j][5], b[j][6], b[j][7]), acc[j], 0, 0, 0);
+            a1, as_bf16x8(S.b[j][4], S.b[j][5], S.b[j][6], S.b[j][7]), acc[j], 0, 0, 0);
       }
     } else if constexpr (WT == WType::kFp8) {
-      i32x8_t a = gload32(a_ptr + aoff + lane_off_a);
-      i32x8_t b[NI];
+      // quantize this lane's 32 activations with the scale of their row's
+      // 128-group (the group spans the 4 lane groups holding the row)
+      float x[32];
 #pragma unroll
-      for (int j = 0; j < NI; ++j) b[j] = gload32(w_ptr[j] + woff);
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = static_cast<uint32_t>(S.a[q][i]);
+          x[8 * q + 2 * i] = __uint_as_float(w << 16);
+          x[8 * q + 2 * i + 1] = __uint_as_float(w & 0xffff0000u);
+        }
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+      amax = fmaxf(amax, __shfl_xor(amax, 16, kWave));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+      const float sa_row = fmaxf(amax, kFp8Eps) / kFp8Max;  // scale of row lane%16
+      const float inv = 1.0f / sa_row;
+      // x / sa_row as the quant pass computes it (correctly rounded): one
+      // FMA-residual correction of x * (1/sa_row) restores the rounding that
+      // the reciprocal product alone misses, so the fp8 codes agree.
+      auto qdiv = [&](float v) {
+        const float q0 = v * inv;
+        const float r = __builtin_fmaf(-q0, sa_row, v);
+        return fminf(fmaxf(__builtin_fmaf(r, inv, q0), -kFp8Max), kFp8Max);
+      };
+      int qa[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(qdiv(x[4 * i]), qdiv(x[4 * i + 1]), 0, false);
+        qa[i] = __builtin_amdgcn_cvt_pk_fp8_f32(qdiv(x[4 * i + 2]), qdiv(x[4 * i + 3]), w, true);
+      }
+      const i32x8_t a = i32x8_t{qa[0], qa[1], qa[2], qa[3], qa[4], qa[5], qa[6], qa[7]};
+      // output rows of this lane are 4*(lane/16) + r: fetch their scales
       float sa[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sa[r] = sa_ptr[r][kt];
+      for (int r = 0; r < 4; ++r) sa[r] = __shfl(sa_row, (lane >> 4) * 4 + r, kWave);
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         f32x4_t t = {0.f, 0.f, 0.f, 0.f};
-        t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[j], t, 0, 0, 0, 0, 0, 0);
+        t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, S.b[j], t, 0, 0, 0, 0, 0, 0);
         const float sb = sb_ptr[j][kt];
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += t[r] * (sa[r] * sb);
       }
     } else {  // int4
-      // activations for this lane: 32 bf16 = elements 32g .. 32g+31 of the stage
-      const uint8_t* ap = a_ptr + aoff + lane_off_a;
-      i32x4_t x4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) x4[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
-      i32x4_t w4[NI];
-#pragma unroll
-      for (int j = 0; j < NI; ++j) w4[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
       f32x4_t t[NI], xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < NI; ++j) t[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
-      // 8 consecutive elements of group d occupy dwords 4d..4d+3 of x (x4[d])
+      // 8 consecutive activations of nibble dword d occupy S.a[d]:
+      // (x0x1)(x2x3)(x4x5)(x6x7) -> reorder to (x0x4)(x1x5)(x2x6)(x3x7)
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const int x01 = x4[d][0], x23 = x4[d][1], x45 = x4[d][2], x67 = x4[d][3];
+        const int x01 = S.a[d][0], x23 = S.a[d][1], x45 = S.a[d][2], x67 = S.a[d][3];
         const int p04 = __builtin_amdgcn_perm(x45, x01, 0x05040100);
         const int p15 = __builtin_amdgcn_perm(x45, x01, 0x07060302);
         const int p26 = __builtin_amdgcn_perm(x67, x23, 0x05040100);
@@ -180,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
         xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs, 0, 0, 0);
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
-          const unsigned wv = static_cast<unsigned>(w4[j][d]);
+          const unsigned wv = static_cast<unsigned>(S.b[j][d]);
           const int b0 = static_cast<int>((wv & 0x000f000fu) | 0x43004300u);
           const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
           const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
@@ -189,8 +239,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
         }
       }
       // fold zero and scale of group kt for this lane's column
-      const int64_t G = p.Kred / 128;
-      const int64_t gbase = (static_cast<int64_t>(e) * G + kt) * p.Nout;
+      const int64_t gbase = (static_cast<int64_t>(e) * (p.Kred / 128) + kt) * p.Nout;
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         const int64_t col = wrow[j];
@@ -200,6 +249,33 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[j][r] - (128.0f + z) * xs[r]);
       }
+    }
+  };
+
+  // split-K range over stages, then interleaved over the 4 waves, PIPE
+  // stages in flight per wave
+  const int per_split = (nk + p.splits - 1) / p.splits;
+  const int k_beg = split * per_split;
+  const int k_end = min(nk, k_beg + per_split);
+  if constexpr (PIPE == 2) {
+    Stage<WT> s0, s1;
+    int kt = k_beg + wid;
+    if (kt < k_end) load(kt, s0);
+    while (kt < k_end) {
+      const int k1 = kt + kWaves;
+      if (k1 < k_end) load(k1, s1);
+      consume(kt, s0);
+      if (k1 >= k_end) break;
+      const int k2 = k1 + kWaves;
+      if (k2 < k_end) load(k2, s0);
+      consume(k1, s1);
+      kt = k2;
+    }
+  } else {
+    for (int kt = k_beg + wid; kt < k_end; kt += kWaves) {
+      Stage<WT> s0;
+      load(kt, s0);
+      consume(kt, s0);
     }
   }
 
@@ -258,7 +334,8 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   dim3 g(static_cast<unsigned>(p.max_tiles), static_cast<unsigned>(p.n_ntiles),
          static_cast<unsigned>(mode == Mode::kGemm2 ? p.splits : 1));
   dim3 b(decode::kThreads);
-#define LAUNCH(WT_, MODE_) decode::gemm_decode_kernel<WT_, MODE_><<<g, b, 0, s>>>(p)
+#define LAUNCH(WT_, MODE_)                                                            \
+  decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_)><<<g, b, 0, s>>>(p)
   if (mode == Mode::kGemm1Silu) {
     switch (wt) {
       case WType::kBf16: LAUNCH(WType::kBf16, Mode::kGemm1Silu); break;

@@ -279,14 +279,17 @@ def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens,
                      ptr(tile_map), ptr(n_tiles), n_tokens, top_k, n_experts, block_m,
                      L.fmoe_max_tiles(n_tokens * top_k, n_experts))
     slots = n_tokens * top_k
+    # fp8: the prefill kernels take pre-quantized activations; the decode
+    # kernels (block_m 16) quantize bf16 rows in-kernel
+    quant_acts = wtype == W_FP8 and block_m != 16
     xa, xs = x, None
-    if wtype == W_FP8:
+    if quant_acts:
         xa, xs = per_token_group_quant_fp8(x, 128)
     act = torch.empty(slots, N, dtype=torch.bfloat16, device=dev)
     check(L.fmoe_gemm1(wtype, ptr(xa), ptr(xs), ptr(w13), ptr(w13_scale), ptr(w13_zp), K, N,
                        ctypes.byref(r), int(apply_router_weight_on_input), ptr(act), 0, st), "gemm1")
     a2, a2s = act, None
-    if wtype == W_FP8:
+    if quant_acts:
         a2, a2s = per_token_group_quant_fp8(act, 128)
     splits = L.fmoe_gemm2_splits(wtype, K, N, ctypes.byref(r), 0)
     y = torch.empty(splits, slots, K, dtype=torch.float32, device=dev)
