@@ -63,11 +63,14 @@ template <>
 struct Stage<WType::kFp8> {
   i32x4_t a[4];   // 32 bf16 of the activation row (quantized in registers)
   i32x8_t b[NI];  // 32 fp8 of each weight row
+  float sb[NI];   // weight block scale of each 16-row block
 };
 template <>
 struct Stage<WType::kInt4> {
   i32x4_t a[4];   // 32 bf16 of the activation row
   i32x4_t b[NI];  // 32 uint4 of each weight row
+  uint16_t sc[NI];  // fp16 group scale of this lane's column
+  uint8_t zb[NI];   // byte holding the group zero of this lane's column
 };
 
 // Stages in flight per wave (see the file comment).
@@ -147,11 +150,21 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
       for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) S.sb[j] = sb_ptr[j][kt];
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
       for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+      // scale and zero of group kt for this lane's column, fetched with the
+      // weights so that the stage's loads complete together
+      const int64_t gbase = (static_cast<int64_t>(e) * (p.Kred / 128) + kt) * p.Nout;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        S.sc[j] = p.b_gscale[gbase + wrow[j]];
+        S.zb[j] = p.b_zero[(gbase >> 1) + (wrow[j] >> 1)];
+      }
     }
   };
 
@@ -208,9 +221,8 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
       for (int j = 0; j < NI; ++j) {
         f32x4_t t = {0.f, 0.f, 0.f, 0.f};
         t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, S.b[j], t, 0, 0, 0, 0, 0, 0);
-        const float sb = sb_ptr[j][kt];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] += t[r] * (sa[r] * sb);
+        for (int r = 0; r < 4; ++r) acc[j][r] += t[r] * (sa[r] * S.sb[j]);
       }
     } else {  // int4
       f32x4_t t[NI], xs = {0.f, 0.f, 0.f, 0.f};
@@ -239,13 +251,11 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
         }
       }
       // fold zero and scale of group kt for this lane's column
-      const int64_t gbase = (static_cast<int64_t>(e) * (p.Kred / 128) + kt) * p.Nout;
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const int64_t col = wrow[j];
-        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, p.b_gscale[gbase + col]));
-        const uint8_t zb = p.b_zero[(gbase >> 1) + (col >> 1)];
-        const float z = static_cast<float>((col & 1) ? (zb >> 4) : (zb & 15));
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, S.sc[j]));
+        const unsigned zb = S.zb[j];
+        const float z = static_cast<float>((wrow[j] & 1) ? (zb >> 4) : (zb & 15));
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[j][r] - (128.0f + z) * xs[r]);
       }
