@@ -8,13 +8,15 @@
 // a_scale[row] * w_scale[block] into the fp32 accumulator).
 //
 // Measured on MI355X, which is what the structure follows:
-//  * LDS: lane-contiguous ds_read_b128 runs at ~2x the rate of any
-//    row-strided pattern.  So a stage is stored "fragment-major": for each
-//    16-row block and each 64-byte half of the row slice, a 1 KiB unit whose
-//    16-byte slot l holds chunk l/16 (of that half) of row l%16.  The MFMA
-//    fragment of lane L is then slot L of the unit: one contiguous read.
-//  * One unit is exactly one global_load_lds_dwordx4 (64 lanes x 16 B), so the
-//    DMA writes it without staging registers or ds_write instructions.
+//  * DMA: global_load_lds_dwordx4 delivers ~2x the bytes per clock when each
+//    4 consecutive lanes read one row's 64 contiguous bytes than when every
+//    lane reads a different row.  LDS: a ds_read_b128 fragment read runs at
+//    full rate only if each 8 consecutive lanes hit 8 distinct 16-byte
+//    columns of a 128-byte window.  A stage is therefore a set of 1 KiB units
+//    (16 rows x 64 bytes of one half of the row slice, 4 lanes per row, the
+//    chunk order XOR-swizzled by row / 2 -- see frag_slot): one unit is one
+//    wave-instruction of DMA, written without staging registers or ds_write,
+//    and every fragment read is conflict-free.
 //  * With the DMA running, operand delivery (not LDS or MFMA issue) bounds
 //    the kernel, so the tile is as large as LDS allows (256 x 256 for bf16:
 //    128 flop per byte moved) and two or three stages are kept in flight.
@@ -90,6 +92,17 @@ __device__ __forceinline__ void dma4(const float* g, float* l) {
                :: "v"(g), "s"(m0) : "memory", "m0");
 }
 
+// Slot of a 1 KiB unit (16 rows x 64 bytes) holding the MFMA fragment of lane
+// L: row L % 16, 16-byte chunk L / 16.  DMA lane i writes slot i with row i / 4,
+// chunk (i % 4) ^ ((row / 2) % 4): the global reads coalesce 4 lanes per row,
+// and every 8 consecutive lanes of a fragment read hit 8 distinct 16-byte
+// columns of a 128-byte window, which ds_read_b128 serves at the contiguous
+// rate (measured: plain row-major or a (row / 4) swizzle run at 70% of it).
+__device__ __forceinline__ int frag_slot(int L) {
+  const int r = L & 15;
+  return 4 * r + ((L >> 4) ^ ((r >> 1) & 3));
+}
+
 __device__ __forceinline__ i32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<const i32x4_t*>(p); }
 
 // Expert e with offs_pad[e] * nn <= key < offs_pad[e + 1] * nn (offs_pad is
@@ -157,7 +170,8 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     return MODE == Mode::kGemm1Silu ? p.topk_indx[s] / p.top_k : s;
   };
   // ---- DMA sources: unit u = NW i + wid -> block u / UPB, half u % UPB;
-  // lane l: row l % 16 of the block, 16-byte chunk 4 half + l / 16.
+  // lane l: row l / 4 of the block, 16-byte chunk 4 half + swz(l) (see
+  // frag_slot), so each 4 consecutive lanes read one row's 64 contiguous bytes.
   const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * kbytes;
   const uint8_t* src[C::UPW];
   int loff[C::UPW];
@@ -165,12 +179,13 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   for (int i = 0; i < C::UPW; ++i) {
     const int u = NW * i + wid;
     const int b = u / UPB, hf = u % UPB;
-    const int coff = (4 * hf + (lane >> 4)) * 16;
+    const int lr = lane >> 2;  // row within the 16-row block
+    const int coff = (4 * hf + ((lane & 3) ^ ((lr >> 1) & 3))) * 16;
     loff[i] = u * kUnit;
     if (i < C::A_UPW) {
-      src[i] = p.A + a_src_row(b * 16 + (lane & 15)) * kbytes + static_cast<int64_t>(k0) * SB + coff;
+      src[i] = p.A + a_src_row(b * 16 + lr) * kbytes + static_cast<int64_t>(k0) * SB + coff;
     } else {
-      const int r = (b - BM / 16) * 16 + (lane & 15);  // row of the B tile
+      const int r = (b - BM / 16) * 16 + lr;  // row of the B tile
       int64_t brow;
       if (MODE == Mode::kGemm1Silu) {
         const int w = r / WN, within = r % WN;
@@ -224,7 +239,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int lane16 = lane * 16;
+  const int lane16 = frag_slot(lane) * 16;
   auto compute = [&](int kt) {
     const uint8_t* st = lds[kt % NBUF];
     const uint8_t* As = st + (wm * MI) * UPB * kUnit + lane16;
