@@ -57,17 +57,17 @@ GemmParams base_params(const fmoe_routing* r) {
 }
 
 // Tile height for the fused path: 16 = decode kernels, else the prefill tile,
-// from the mean slots per expert: bf16 256-row tiles (the most efficient
-// prefill tile) once experts average >= 384 slots, 128 from 96, else 64; fp8
-// tiles stop at 128 rows (LDS holds three 128-byte stages of 128x256).
+// from the mean slots per expert (measured on the BASELINE shapes): bf16
+// 256-row tiles once experts average >= 256 slots, 128-row tiles from 40
+// (a half-empty 128-row tile still beats a 64-row one), else 64.
 int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
   const int64_t slots = M * k;
   const int64_t active = slots < E ? slots : E;
   if (wtype == FMOE_W_INT4 || path == 2) return kDecodeBM;
   if (path != 1 && slots <= kDecodeBM * (active > 0 ? active : 1)) return kDecodeBM;
   const int64_t mean = slots / E;
-  if (wtype == FMOE_W_BF16 && mean >= 384) return 256;
-  return mean >= 96 ? 128 : 64;
+  if (wtype == FMOE_W_BF16 && mean >= 256) return 256;
+  return mean >= 40 ? 128 : 64;
 }
 
 }  // namespace

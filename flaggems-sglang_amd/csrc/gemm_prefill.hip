@@ -2,21 +2,20 @@
 // LDS stages filled by direct-to-LDS DMA.
 //
 // Workgroup = 8 waves (512 threads) laid out WAVES_M x WAVES_N; tile BM x BN;
-// SB bytes of the reduction dim per row per stage (bf16: SB = 64 -> 32
-// elements, one v_mfma_f32_16x16x32_bf16 step; fp8: SB = 128 -> one 128-wide
+// SB bytes of the reduction dim per row per stage (bf16: SB = 64 or 128 ->
+// one or two v_mfma_f32_16x16x32_bf16 steps; fp8: SB = 128 -> one 128-wide
 // scale block, one v_mfma_f32_16x16x128_f8f6f4 with its result scaled by
 // a_scale[row] * w_scale[block] into the fp32 accumulator).
 //
 // Measured on MI355X, which is what the structure follows:
-//  * DMA: global_load_lds_dwordx4 delivers ~2x the bytes per clock when each
-//    4 consecutive lanes read one row's 64 contiguous bytes than when every
-//    lane reads a different row.  LDS: a ds_read_b128 fragment read runs at
-//    full rate only if each 8 consecutive lanes hit 8 distinct 16-byte
-//    columns of a 128-byte window.  A stage is therefore a set of 1 KiB units
-//    (16 rows x 64 bytes of one half of the row slice, 4 lanes per row, the
-//    chunk order XOR-swizzled by row / 2 -- see frag_slot): one unit is one
-//    wave-instruction of DMA, written without staging registers or ds_write,
-//    and every fragment read is conflict-free.
+//  * DMA: global_load_lds_dwordx4 delivers ~2x the bytes per clock when
+//    consecutive lanes read one row's contiguous bytes (4 or 8 lanes x 16 B)
+//    than when every lane reads a different row.  LDS: a ds_read_b128
+//    fragment read runs at full rate only if each 8 consecutive lanes hit 8
+//    distinct 16-byte columns of a 128-byte window.  A stage is therefore a
+//    set of 1 KiB units in row-major, XOR-swizzled layouts (see frag_off):
+//    one unit is one wave-instruction of DMA, written without staging
+//    registers or ds_write, and every fragment read is conflict-free.
 //  * With the DMA running, operand delivery (not LDS or MFMA issue) bounds
 //    the kernel, so the tile is as large as LDS allows (256 x 256 for bf16:
 //    128 flop per byte moved) and two or three stages are kept in flight.
@@ -56,6 +55,7 @@ struct Cfg {
   static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   static constexpr int MI = WM / 16, NI = WN / 16;
   static constexpr int UPB = SB / 64;                       // units per 16-row block
+  static_assert(SB == 64 || SB == 128, "stage width");
   static constexpr int A_UNITS = (BM / 16) * UPB, B_UNITS = (BN / 16) * UPB;
   static constexpr int UPW = (A_UNITS + B_UNITS) / NW;      // DMA per wave per stage
   static constexpr int A_UPW = A_UNITS / NW;
@@ -92,15 +92,24 @@ __device__ __forceinline__ void dma4(const float* g, float* l) {
                :: "v"(g), "s"(m0) : "memory", "m0");
 }
 
-// Slot of a 1 KiB unit (16 rows x 64 bytes) holding the MFMA fragment of lane
-// L: row L % 16, 16-byte chunk L / 16.  DMA lane i writes slot i with row i / 4,
-// chunk (i % 4) ^ ((row / 2) % 4): the global reads coalesce 4 lanes per row,
-// and every 8 consecutive lanes of a fragment read hit 8 distinct 16-byte
-// columns of a 128-byte window, which ds_read_b128 serves at the contiguous
-// rate (measured: plain row-major or a (row / 4) swizzle run at 70% of it).
-__device__ __forceinline__ int frag_slot(int L) {
+// LDS unit layouts (1 KiB = one DMA wave-instruction, lane i -> bytes 16i):
+//  * 64-byte stages: a unit is 16 rows x 64 bytes; DMA lane i reads row i / 4,
+//    chunk (i % 4) ^ ((row / 2) % 4), so 4 consecutive lanes read one row's 64
+//    contiguous bytes.
+//  * 128-byte stages: a unit is 8 rows x 128 bytes (rows 0-7 or 8-15 of a
+//    16-row block); DMA lane i reads row i / 8, chunk (i % 8) ^ (row), so 8
+//    consecutive lanes read one row's 128 contiguous bytes.
+// The MFMA fragment of lane L is row L % 16, 16-byte chunk c (c = L / 16, and
+// for 128-byte stages also 4 + L / 16); with the swizzles above every 8
+// consecutive lanes of a fragment read hit 8 distinct 16-byte columns of a
+// 128-byte window, which ds_read_b128 serves at the contiguous rate
+// (measured: plain row-major or a (row / 4) swizzle run at 70% of it).
+template <int SB>
+__device__ __forceinline__ int frag_off(int L, int c) {
   const int r = L & 15;
-  return 4 * r + ((L >> 4) ^ ((r >> 1) & 3));
+  if constexpr (SB == 64) return 16 * (4 * r + (c ^ ((r >> 1) & 3)));
+  const int ru = r & 7;
+  return (r >> 3) * 1024 + 16 * (8 * ru + (c ^ ru));
 }
 
 __device__ __forceinline__ i32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<const i32x4_t*>(p); }
@@ -169,18 +178,24 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     if (s >= row_end) s = row_beg;  // padding row: any valid row, result discarded
     return MODE == Mode::kGemm1Silu ? p.topk_indx[s] / p.top_k : s;
   };
-  // ---- DMA sources: unit u = NW i + wid -> block u / UPB, half u % UPB;
-  // lane l: row l / 4 of the block, 16-byte chunk 4 half + swz(l) (see
-  // frag_slot), so each 4 consecutive lanes read one row's 64 contiguous bytes.
+  // ---- DMA sources: unit u = NW i + wid of the stage (A units first, then
+  // B units) in the layout of frag_off.
   const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * kbytes;
   const uint8_t* src[C::UPW];
   int loff[C::UPW];
 #pragma unroll
   for (int i = 0; i < C::UPW; ++i) {
     const int u = NW * i + wid;
-    const int b = u / UPB, hf = u % UPB;
-    const int lr = lane >> 2;  // row within the 16-row block
-    const int coff = (4 * hf + ((lane & 3) ^ ((lr >> 1) & 3))) * 16;
+    const int b = u / UPB;
+    int lr, coff;  // row within the 16-row block, byte offset in the row slice
+    if constexpr (SB == 64) {
+      lr = lane >> 2;
+      coff = ((lane & 3) ^ ((lr >> 1) & 3)) * 16;
+    } else {
+      const int ru = lane >> 3;
+      lr = (u % 2) * 8 + ru;
+      coff = ((lane & 7) ^ ru) * 16;
+    }
     loff[i] = u * kUnit;
     if (i < C::A_UPW) {
       src[i] = p.A + a_src_row(b * 16 + lr) * kbytes + static_cast<int64_t>(k0) * SB + coff;
@@ -239,21 +254,23 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int lane16 = frag_slot(lane) * 16;
+  // per-lane fragment offsets within a 16-row block's units
+  const int foff0 = frag_off<SB>(lane, lane >> 4);
+  const int foff1 = SB == 64 ? 0 : frag_off<SB>(lane, 4 + (lane >> 4));
   auto compute = [&](int kt) {
     const uint8_t* st = lds[kt % NBUF];
-    const uint8_t* As = st + (wm * MI) * UPB * kUnit + lane16;
-    const uint8_t* Bs = st + (C::A_UNITS + wn * NI * UPB) * kUnit + lane16;
+    const uint8_t* As = st + (wm * MI) * UPB * kUnit;
+    const uint8_t* Bs = st + (C::A_UNITS + wn * NI * UPB) * kUnit;
     if constexpr (FP8) {
       i32x8_t fa[MI], fb[NI];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        i32x4_t lo = lds16(As + (2 * i) * kUnit), hi = lds16(As + (2 * i + 1) * kUnit);
+        i32x4_t lo = lds16(As + (2 * i) * kUnit + foff0), hi = lds16(As + (2 * i) * kUnit + foff1);
         fa[i] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        i32x4_t lo = lds16(Bs + (2 * j) * kUnit), hi = lds16(Bs + (2 * j + 1) * kUnit);
+        i32x4_t lo = lds16(Bs + (2 * j) * kUnit + foff0), hi = lds16(Bs + (2 * j) * kUnit + foff1);
         fb[j] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
       const float sb0 = sb_lds[wn][0][kt], sb1 = sb_lds[wn][1][kt];
@@ -274,14 +291,15 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       }
     } else {
 #pragma unroll
-      for (int hf = 0; hf < UPB; ++hf) {
+      for (int h = 0; h < UPB; ++h) {  // 32-element k-steps of the stage
+        const int fo = h == 0 ? foff0 : foff1;
         bf16x8_t fa[MI], fb[NI];
 #pragma unroll
         for (int i = 0; i < MI; ++i)
-          fa[i] = __builtin_bit_cast(bf16x8_t, lds16(As + (i * UPB + hf) * kUnit));
+          fa[i] = __builtin_bit_cast(bf16x8_t, lds16(As + i * UPB * kUnit + fo));
 #pragma unroll
         for (int j = 0; j < NI; ++j)
-          fb[j] = __builtin_bit_cast(bf16x8_t, lds16(Bs + (j * UPB + hf) * kUnit));
+          fb[j] = __builtin_bit_cast(bf16x8_t, lds16(Bs + j * UPB * kUnit + fo));
 #pragma unroll
         for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -363,8 +381,8 @@ int launch(const GemmParams& p0, hipStream_t s) {
 }  // namespace prefill
 
 // Host launcher: picks the instantiation for the tile height.
-//   bf16: BM 256 -> 256x256, 4x2 waves, 64-byte stages, 3-deep ring
-//         BM 128 -> 128x256, 2x4 waves, 64-byte stages, 4-deep ring
+//   bf16: BM 256 -> 256x256, 4x2 waves, 128-byte stages, 2-deep ring
+//         BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM  64 ->  64x256, 1x4 waves, 64-byte stages, 4-deep ring
 //   fp8 : BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM  64 ->  64x256, 1x8 waves, 128-byte stages, 3-deep ring
@@ -375,8 +393,8 @@ int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t
   (mode == Mode::kGemm1Silu ? launch<Cfg<BM, BN, WMS, WNS, SB, NB, F8, Mode::kGemm1Silu>>(p, s) \
                             : launch<Cfg<BM, BN, WMS, WNS, SB, NB, F8, Mode::kGemm2>>(p, s))
   if (!fp8) {
-    if (bm == 256) return L(256, 256, 4, 2, 64, 3, false);
-    if (bm == 128) return L(128, 256, 2, 4, 64, 4, false);
+    if (bm == 256) return L(256, 256, 4, 2, 128, 2, false);
+    if (bm == 128) return L(128, 256, 2, 4, 128, 3, false);
     if (bm == 64) return L(64, 256, 1, 4, 64, 4, false);
   } else {
     if (bm == 128) return L(128, 256, 2, 4, 128, 3, true);

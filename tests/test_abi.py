@@ -45,7 +45,8 @@ def test_host_queries():
     assert L.fmoe_choose_block_m(_lib.W_INT4, 4096, 2, 8, 0) == 16
     assert L.fmoe_choose_block_m(_lib.W_BF16, 1, 2, 8, 0) == 16
     assert L.fmoe_choose_block_m(_lib.W_BF16, 4096, 2, 8, 0) == 256
-    assert L.fmoe_choose_block_m(_lib.W_BF16, 1024, 8, 128, 0) == 64
+    assert L.fmoe_choose_block_m(_lib.W_BF16, 1024, 8, 128, 0) == 128
+    assert L.fmoe_choose_block_m(_lib.W_BF16, 400, 8, 128, 0) == 64
     assert L.fmoe_choose_block_m(_lib.W_FP8, 4096, 8, 256, 0) == 128
 
 
