@@ -162,8 +162,11 @@ typedef struct fmoe_routing {
  * + _silu_and_mul_triton (ops/fused_moe.py:189-202).  For every sorted slot
  * s of expert e:  inter = bf16(x[token(s)] @ w13[e]^T  [* gate_scal[s] when
  * gamma_on_input]);  act[s, j] = bf16(silu(inter[j]) * inter[N + j]).
- * act: [M*k, N] bf16 in sorted-slot order.  fp8: x is fp8 [M, K] with
- * x_scale [M, K/128]; int4: w13_scale/w13_zero as in the header comment.
+ * act: [M*k, N] bf16 in sorted-slot order.  fp8 with prefill routing
+ * (block_m >= 64): x is fp8 [M, K] with x_scale [M, K/128]; fp8 with decode
+ * routing (block_m 16): x is bf16 and x_scale must be null (rows are
+ * quantized in the kernel, bit-identical to fmoe_quant_fp8_group); int4:
+ * w13_scale/w13_zero as in the header comment.
  * Requires K % 128 == 0, N % 128 == 0 (int4: group == 128). */
 int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const void* w13,
                const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
@@ -174,7 +177,9 @@ int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const void* w13,
  * [* gate_scal[s] when apply_gamma], fp32, sorted-slot order.  `splits`
  * partial sums over the reduction dim N are written to y[0..splits-1]
  * (fmoe_gemm2_splits() gives the count the library picks; every plane is
- * written, so y needs no clearing). */
+ * written, so y needs no clearing).  fp8 activations follow fmoe_gemm1:
+ * fp8 act + act_scale with prefill routing, bf16 act + null act_scale with
+ * decode routing. */
 int fmoe_gemm2(int wtype, const void* act, const float* act_scale, const void* w2,
                const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
                const fmoe_routing* r, int apply_gamma, float* y, int splits, int path,
@@ -182,7 +187,7 @@ int fmoe_gemm2(int wtype, const void* act, const float* act_scale, const void* w
 int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_routing* r, int path);
 
 /* Tile height the library pairs with the GEMM kernels for a problem size:
- * 16 selects the decode (streaming) kernels, 64 / 128 the prefill kernels.
+ * 16 selects the decode (streaming) kernels, 64 / 128 / 256 the prefill kernels.
  * path: 0 = choose, 1 = prefill, 2 = decode (int4 is decode-only). */
 int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path);
 
