@@ -127,6 +127,38 @@ __device__ __forceinline__ int find_expert(const int32_t* offs_pad, int E, int k
   return base + (63 - __builtin_clzll(b));
 }
 
+// 4x4 transpose across each quad of lanes (q = lane % 4): on entry v[r] of
+// lane q is element (column q, row r), on exit v[c] is element (column c,
+// row q).  Two exchange steps (lane bit 0 with element bit 0, then bit 1),
+// each two DPP quad permutes.
+template <int CTRL>
+__device__ __forceinline__ float qperm(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ void quad_transpose(f32x4_t& v, int lane) {
+  const bool p0 = lane & 1, p1 = lane & 2;
+  float s0 = p0 ? v[0] : v[1], s1 = p0 ? v[2] : v[3];
+  float r0 = qperm<0xB1>(s0), r1 = qperm<0xB1>(s1);  // quad_perm [1,0,3,2]
+  if (p0) {
+    v[0] = r0;
+    v[2] = r1;
+  } else {
+    v[1] = r0;
+    v[3] = r1;
+  }
+  s0 = p1 ? v[0] : v[2];
+  s1 = p1 ? v[1] : v[3];
+  r0 = qperm<0x4E>(s0);  // quad_perm [2,3,0,1]
+  r1 = qperm<0x4E>(s1);
+  if (p1) {
+    v[0] = r0;
+    v[1] = r1;
+  } else {
+    v[2] = r0;
+    v[3] = r1;
+  }
+}
+
 template <class C>
 __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, MI = C::MI, NI = C::NI;
@@ -329,32 +361,44 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   }
 
   // ---- epilogue.  C layout of a 16x16 block: lane holds column lane%16,
-  // rows 4*(lane/16) + r.
-  const int col16 = lane & 15;
+  // rows 4*(lane/16) + r.  A 4x4 transpose inside each quad of lanes turns
+  // that into row 4*(lane/16) + lane%4, columns 4*((lane/4)%4) + 0..3, so each
+  // lane stores 4 consecutive outputs at once (8 or 16 bytes) instead of 4
+  // scattered ones.
+  const int orow = (lane >> 4) * 4 + (lane & 3);   // row within the 16x16 block
+  const int ocol = ((lane >> 2) & 3) * 4;          // first of the lane's 4 columns
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
+    const int s = row_beg + wm * WM + i * 16 + orow;
+    const bool ok = s < row_end;
+    const float g = (p.gamma && ok) ? p.gate_scal[s] : 1.0f;
+    if (MODE == Mode::kGemm1Silu) {
+      uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.N_act;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int s = row_beg + wm * WM + i * 16 + (lane >> 4) * 4 + r;
-      if (s >= row_end) continue;
-      const float g = p.gamma ? p.gate_scal[s] : 1.0f;
-      if (MODE == Mode::kGemm1Silu) {
-        uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.N_act;
+      for (int j = 0; j < NI / 2; ++j) {
+        f32x4_t gv = acc[i][j], uv = acc[i][j + NI / 2];
+        quad_transpose(gv, lane);
+        quad_transpose(uv, lane);
+        uint32_t w[2];
 #pragma unroll
-        for (int j = 0; j < NI / 2; ++j) {
-          const float gv = round_bf16(acc[i][j][r] * g);
-          const float uv = round_bf16(acc[i][j + NI / 2][r] * g);
-          const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2) + j * 16 + col16;
-          act[col] = f32_to_bf16(silu_mul(gv, uv));
+        for (int c = 0; c < 2; ++c) {
+          const float a0 = silu_mul(round_bf16(gv[2 * c] * g), round_bf16(uv[2 * c] * g));
+          const float a1 = silu_mul(round_bf16(gv[2 * c + 1] * g), round_bf16(uv[2 * c + 1] * g));
+          w[c] = f32_to_bf16(a0) | (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
         }
-      } else {
-        float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
-                   static_cast<int64_t>(s) * p.Nout;
+        const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2) + j * 16 + ocol;
+        if (ok) *reinterpret_cast<uint2*>(act + col) = make_uint2(w[0], w[1]);
+      }
+    } else {
+      float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
+                 static_cast<int64_t>(s) * p.Nout;
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + col16;
-          if (col < p.Nout) y[col] = acc[i][j][r] * g;
-        }
+      for (int j = 0; j < NI; ++j) {
+        f32x4_t v = acc[i][j];
+        quad_transpose(v, lane);
+        const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + ocol;
+        if (ok && col < p.Nout)
+          *reinterpret_cast<float4*>(y + col) = make_float4(v[0] * g, v[1] * g, v[2] * g, v[3] * g);
       }
     }
   }
