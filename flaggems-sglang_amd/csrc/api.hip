@@ -53,6 +53,10 @@ GemmParams base_params(const fmoe_routing* r) {
   p.n_experts = r->n_experts;
   p.max_tiles = r->max_tiles;
   p.splits = 1;
+  p.act = FMOE_ACT_SILU;
+  p.bias = nullptr;
+  p.alpha = 1.0f;
+  p.limit = 0.0f;
   return p;
 }
 
@@ -110,6 +114,29 @@ extern "C" int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const 
                           const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
                           const fmoe_routing* r, int gamma_on_input, void* act, int path,
                           void* stream) {
+  return fmoe_gemm1_ex(wtype, x, x_scale, w13, w13_scale, w13_zero, K, N, r, gamma_on_input,
+                       nullptr, act, path, stream);
+}
+
+namespace {
+int check_epilogue(const fmoe_epilogue* ep, const char* who) {
+  if (!ep) return FMOE_OK;
+  if (ep->activation != FMOE_ACT_SILU && ep->activation != FMOE_ACT_GELU &&
+      ep->activation != FMOE_ACT_SWIGLU)
+    return fail(FMOE_ERR_INVALID, "%s: unknown activation %d", who, ep->activation);
+  if (ep->bias && ep->activation != FMOE_ACT_SWIGLU)
+    return fail(FMOE_ERR_UNSUPPORTED, "%s: bias with this activation is not supported", who);
+  if (!(ep->alpha == ep->alpha) || !(ep->limit == ep->limit))
+    return fail(FMOE_ERR_INVALID, "%s: alpha / limit must not be NaN", who);
+  return FMOE_OK;
+}
+}  // namespace
+
+extern "C" int fmoe_gemm1_ex(int wtype, const void* x, const float* x_scale, const void* w13,
+                             const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
+                             const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep,
+                             void* act, int path, void* stream) {
+  if (int st = check_epilogue(ep, "gemm1")) return st;
   if (int st = check_routing(r, "gemm1")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm1: unknown weight type %d", wtype);
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
@@ -140,6 +167,12 @@ extern "C" int fmoe_gemm1(int wtype, const void* x, const float* x_scale, const 
   p.N_act = N;
   p.gamma = gamma_on_input;
   p.out = act;
+  if (ep) {
+    p.act = ep->activation;
+    p.bias = ep->bias;
+    p.alpha = ep->alpha;
+    p.limit = ep->limit;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (is_decode(r)) return launch_decode(to_wt(wtype), Mode::kGemm1Silu, p, s);
   return launch_prefill(to_wt(wtype), Mode::kGemm1Silu, r->block_m, p, s);
@@ -149,6 +182,14 @@ extern "C" int fmoe_gemm2(int wtype, const void* act, const float* act_scale, co
                           const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
                           const fmoe_routing* r, int apply_gamma, float* y, int splits, int path,
                           void* stream) {
+  return fmoe_gemm2_ex(wtype, act, act_scale, w2, w2_scale, w2_zero, K, N, r, apply_gamma, nullptr,
+                       y, splits, path, stream);
+}
+
+extern "C" int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale, const void* w2,
+                             const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
+                             const fmoe_routing* r, int apply_gamma, const float* bias, float* y,
+                             int splits, int path, void* stream) {
   if (int st = check_routing(r, "gemm2")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm2: unknown weight type %d", wtype);
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
@@ -180,6 +221,7 @@ extern "C" int fmoe_gemm2(int wtype, const void* act, const float* act_scale, co
   p.Nout = K;
   p.N_act = N;
   p.gamma = apply_gamma;
+  p.bias = bias;
   p.out = y;
   p.splits = splits;
   p.out_split_stride = r->n_tokens * r->top_k * K;
@@ -212,6 +254,8 @@ int check_fused(const fmoe_fused_args* a) {
                 a->group_size);
   if (a->path < 0 || a->path > 2) return fail(FMOE_ERR_INVALID, "fused_experts: path %d", a->path);
   if (a->M > 65535) return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: M > 65535 is not supported");
+  fmoe_epilogue ep{a->activation, a->b13, a->alpha, a->limit};
+  if (int st = check_epilogue(&ep, "fused_experts")) return st;
   return FMOE_OK;
 }
 
@@ -315,8 +359,9 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
     x = at(L.xq);
     xs = static_cast<const float*>(at(L.xs));
   }
-  if (int st = fmoe_gemm1(a->wtype, x, xs, a->w13, a->w13_scale, a->w13_zero, a->K, a->N, &r,
-                          a->apply_router_weight_on_input, at(L.act), 0, stream))
+  fmoe_epilogue ep{a->activation, a->b13, a->alpha, a->limit};
+  if (int st = fmoe_gemm1_ex(a->wtype, x, xs, a->w13, a->w13_scale, a->w13_zero, a->K, a->N, &r,
+                             a->apply_router_weight_on_input, &ep, at(L.act), 0, stream))
     return st;
   const void* act = at(L.act);
   const float* acts = nullptr;
@@ -327,9 +372,9 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
     act = at(L.actq);
     acts = static_cast<const float*>(at(L.acts));
   }
-  if (int st = fmoe_gemm2(a->wtype, act, acts, a->w2, a->w2_scale, a->w2_zero, a->K, a->N, &r,
-                          !a->apply_router_weight_on_input, static_cast<float*>(at(L.y)), L.splits,
-                          0, stream))
+  if (int st = fmoe_gemm2_ex(a->wtype, act, acts, a->w2, a->w2_scale, a->w2_zero, a->K, a->N, &r,
+                             !a->apply_router_weight_on_input, a->b2, static_cast<float*>(at(L.y)),
+                             L.splits, 0, stream))
     return st;
   return fmoe_moe_sum(static_cast<const float*>(at(L.y)), L.splits, o.gate_indx, a->M, a->top_k,
                       a->K, a->routed_scaling_factor, a->out, stream);

@@ -34,9 +34,52 @@ struct GemmParams {
   int n_ntiles;            // output tiles along Nout
   int splits;              // GEMM2 split-K factor (decode path)
   int group_tiles;         // prefill: concurrent tiles per rasterization window (0 = default)
+  // epilogue (fmoe_epilogue): activation, fp32 bias [E, Nout], swiglu alpha / limit
+  int act;
+  const float* bias;
+  float alpha;
+  float limit;
 };
+
+enum Act { kActSilu = 0, kActGelu = 1, kActSwiglu = 2 };
 
 enum class Mode { kGemm1Silu, kGemm2 };
 enum class WType { kBf16, kFp8, kInt4 };
+
+// Weight row of GEMM1 output column c: gate (u = 0) or up / linear (u = 1).
+// SiLU and GELU use split halves (gate c, up N + c), SWIGLU interleaved rows
+// (gate 2c, linear 2c + 1).
+__host__ __device__ __forceinline__ int64_t gemm1_row(int act, int64_t n_act, int64_t c, int u) {
+  return act == kActSwiglu ? 2 * c + u : c + u * n_act;
+}
+
+// GEMM1 epilogue value for output column c of a slot: ga / ua are the fp32
+// GEMM results of its gate and up (linear) rows, gb / ub their biases, g the
+// routing weight when applied on the input (else 1).
+__device__ __forceinline__ float gemm1_act(const GemmParams& p, float ga, float ua, float gb,
+                                           float ub, float g) {
+  if (p.act == kActSwiglu) {
+    float gv = ga + gb, lv = ua + ub;
+    if (p.limit > 0.f) {
+      gv = fminf(gv, p.limit);
+      lv = fminf(fmaxf(lv, -p.limit), p.limit);
+    }
+    return gv / (1.0f + __expf(-p.alpha * gv)) * (lv + 1.0f) * g;
+  }
+  const float gv = round_bf16(ga * g), uv = round_bf16(ua * g);
+  if (p.act == kActGelu) return 0.5f * gv * (1.0f + erff(gv * 0.7071067811865476f)) * uv;
+  return silu_mul(gv, uv);
+}
+
+// GEMM1 biases of output column c of expert e (0 without a bias).
+__device__ __forceinline__ void gemm1_bias(const GemmParams& p, int e, int64_t c, float& gb,
+                                           float& ub) {
+  gb = ub = 0.f;
+  if (p.bias) {
+    const float* b = p.bias + static_cast<int64_t>(e) * p.Nout;
+    gb = b[gemm1_row(p.act, p.N_act, c, 0)];
+    ub = b[gemm1_row(p.act, p.N_act, c, 1)];
+  }
+}
 
 }  // namespace fmoe

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
     int64_t r;
     if (MODE == Mode::kGemm1Silu) {
       int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + (lane & 15);
-      r = j < NI / 2 ? jj : p.N_act + jj;
+      r = gemm1_row(p.act, p.N_act, jj, j < NI / 2 ? 0 : 1);
     } else {
       r = static_cast<int64_t>(nt) * BN + j * 16 + (lane & 15);
       if (r >= p.Nout) r = p.Nout - 1;
@@ -125,13 +125,13 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 #pragma unroll
   for (int j = 0; j < NI; ++j) w_ptr[j] = Be + wrow[j] * w_bytes + lane_off_w;
 
-  // fp8 weight-scale rows (16-row blocks never straddle a 128-row block)
+  // fp8 weight-scale row of each lane's weight rows
   const int ksb = static_cast<int>(p.Kred / 128);
   const float* sb_ptr[NI] = {};
   if (kFp8) {
     const float* se = p.b_scale + static_cast<int64_t>(e) * (p.Nout / 128) * ksb;
 #pragma unroll
-    for (int j = 0; j < NI; ++j) sb_ptr[j] = se + ((wrow[j] - (lane & 15)) / 128) * ksb;
+    for (int j = 0; j < NI; ++j) sb_ptr[j] = se + (wrow[j] / 128) * ksb;
   }
 
   f32x4_t acc[NI];
@@ -316,10 +316,10 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
       uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.N_act;
 #pragma unroll
       for (int j = 0; j < NI / 2; ++j) {
-        const float gv = round_bf16(acc[j][r] * g);
-        const float uv = round_bf16(acc[j + NI / 2][r] * g);
         const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + j * 16 + col16;
-        act[col] = f32_to_bf16(silu_mul(gv, uv));
+        float gb, ub;
+        gemm1_bias(p, e, col, gb, ub);
+        act[col] = f32_to_bf16(gemm1_act(p, acc[j][r], acc[j + NI / 2][r], gb, ub, g));
       }
     } else {
       float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
@@ -327,7 +327,10 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         const int64_t col = static_cast<int64_t>(nt) * BN + j * 16 + col16;
-        if (col < p.Nout) y[col] = acc[j][r] * g;
+        if (col < p.Nout) {
+          const float b = (p.bias && split == 0) ? p.bias[static_cast<int64_t>(e) * p.Nout + col] : 0.f;
+          y[col] = (acc[j][r] + b) * g;
+        }
       }
     }
   }

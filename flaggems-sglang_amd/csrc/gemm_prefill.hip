@@ -237,7 +237,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       if (MODE == Mode::kGemm1Silu) {
         const int w = r / WN, within = r % WN;
         const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + w * (WN / 2) + (within % (WN / 2));
-        brow = within < WN / 2 ? j : p.N_act + j;
+        brow = gemm1_row(p.act, p.N_act, j, within < WN / 2 ? 0 : 1);
       } else {
         brow = static_cast<int64_t>(nt) * BN + r;
         if (brow >= p.Nout) brow = p.Nout - 1;
@@ -255,9 +255,10 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     const float* s0;
     const float* s1;
     if (MODE == Mode::kGemm1Silu) {
+      // the wave's gate rows (and up rows) lie in one 128-row scale block
       const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2);
-      s0 = se + (j / 128) * ksb;
-      s1 = se + ((p.N_act + j) / 128) * ksb;
+      s0 = se + (gemm1_row(p.act, p.N_act, j, 0) / 128) * ksb;
+      s1 = se + (gemm1_row(p.act, p.N_act, j, 1) / 128) * ksb;
     } else {
       int64_t j = static_cast<int64_t>(nt) * BN + wn * WN;
       if (j >= p.Nout) j = p.Nout - 1;
@@ -380,13 +381,18 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
         quad_transpose(gv, lane);
         quad_transpose(uv, lane);
         uint32_t w[2];
+        const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2) + j * 16 + ocol;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const float a0 = silu_mul(round_bf16(gv[2 * c] * g), round_bf16(uv[2 * c] * g));
-          const float a1 = silu_mul(round_bf16(gv[2 * c + 1] * g), round_bf16(uv[2 * c + 1] * g));
-          w[c] = f32_to_bf16(a0) | (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
+          float a[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            float gb, ub;
+            gemm1_bias(p, e, col + 2 * c + h, gb, ub);
+            a[h] = gemm1_act(p, gv[2 * c + h], uv[2 * c + h], gb, ub, g);
+          }
+          w[c] = f32_to_bf16(a[0]) | (static_cast<uint32_t>(f32_to_bf16(a[1])) << 16);
         }
-        const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2) + j * 16 + ocol;
         if (ok) *reinterpret_cast<uint2*>(act + col) = make_uint2(w[0], w[1]);
       }
     } else {
@@ -397,6 +403,11 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
         f32x4_t v = acc[i][j];
         quad_transpose(v, lane);
         const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + ocol;
+        if (p.bias && split == 0 && col < p.Nout) {
+          const float* b = p.bias + static_cast<int64_t>(e) * p.Nout + col;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] += b[c];
+        }
         if (ok && col < p.Nout)
           *reinterpret_cast<float4*>(y + col) = make_float4(v[0] * g, v[1] * g, v[2] * g, v[3] * g);
       }

@@ -41,6 +41,6 @@ const char* fmoe_status_string(int status) {
 
 const char* fmoe_last_error(void) { return g_last_error; }
 
-int fmoe_abi_version(void) { return 1; }
+int fmoe_abi_version(void) { return 2; }
 
 }  // extern "C"

@@ -23,6 +23,7 @@ FMOE_ERR_WORKSPACE = 3
 FMOE_ERR_HIP = 4
 
 W_BF16, W_FP8, W_INT4 = 0, 1, 2
+ACT_SILU, ACT_GELU, ACT_SWIGLU = 0, 1, 2
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)
 c_f32p = ctypes.POINTER(ctypes.c_float)
@@ -44,6 +45,11 @@ class Routing(ctypes.Structure):
     ]
 
 
+class Epilogue(ctypes.Structure):
+    _fields_ = [("activation", ctypes.c_int32), ("bias", vp), ("alpha", ctypes.c_float),
+                ("limit", ctypes.c_float)]
+
+
 class FusedArgs(ctypes.Structure):
     _fields_ = [
         ("wtype", ctypes.c_int32), ("x", vp), ("M", ctypes.c_int64), ("K", ctypes.c_int64),
@@ -52,6 +58,8 @@ class FusedArgs(ctypes.Structure):
         ("group_size", ctypes.c_int32), ("topk_weights", vp), ("topk_ids", vp),
         ("apply_router_weight_on_input", ctypes.c_int32), ("routed_scaling_factor", ctypes.c_float),
         ("path", ctypes.c_int32), ("out", vp), ("workspace", vp), ("workspace_bytes", ctypes.c_size_t),
+        ("activation", ctypes.c_int32), ("b13", vp), ("b2", vp), ("alpha", ctypes.c_float),
+        ("limit", ctypes.c_float),
     ]
 
 
@@ -74,6 +82,12 @@ _SIGS = {
                                   ctypes.POINTER(Routing), ctypes.c_int, vp, ctypes.c_int, vp]),
     "fmoe_gemm2": (ctypes.c_int, [ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int64,
                                   ctypes.POINTER(Routing), ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, vp]),
+    "fmoe_gemm1_ex": (ctypes.c_int, [ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int64,
+                                     ctypes.POINTER(Routing), ctypes.c_int, ctypes.POINTER(Epilogue), vp,
+                                     ctypes.c_int, vp]),
+    "fmoe_gemm2_ex": (ctypes.c_int, [ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int64,
+                                     ctypes.POINTER(Routing), ctypes.c_int, vp, vp, ctypes.c_int,
+                                     ctypes.c_int, vp]),
     "fmoe_gemm2_splits": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.POINTER(Routing), ctypes.c_int]),
     "fmoe_choose_block_m": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int]),

@@ -265,11 +265,24 @@ def _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w
     return W_BF16
 
 
+_ACTIVATIONS = {"silu": _lib.ACT_SILU, "gelu": _lib.ACT_GELU}
+
+
+def _act_code(activation: str) -> int:
+    """silu / gelu (ops/fused_moe.py:198-206); anything else raises the
+    reference's ValueError."""
+    if activation not in _ACTIVATIONS:
+        raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+    return _ACTIVATIONS[activation]
+
+
 def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens, top_k,
                 n_experts, topk_indx, gate_indx, gate_scal, offs_raw, offs_pad, tile_map, n_tiles,
-                block_m, apply_router_weight_on_input, scale, combine=True):
-    """GEMM1+SiLU -> GEMM2 -> top-k sum on prepared routing, SGLang layouts
-    ``w13 [E, 2N, K]``, ``w2 [E, K, N]``."""
+                block_m, apply_router_weight_on_input, scale, combine=True, act=_lib.ACT_SILU,
+                b13=None, b2=None, alpha=1.0, limit=0.0):
+    """GEMM1+activation -> GEMM2 -> top-k sum on prepared routing, SGLang
+    layouts ``w13 [E, 2N, K]``, ``w2 [E, K, N]``; ``b13 [E, 2N]`` / ``b2 [E, K]``
+    fp32 biases (bias path)."""
     L = lib()
     M, K = x.shape
     N = w2.shape[2] * (2 if wtype == W_INT4 else 1)
@@ -285,17 +298,19 @@ def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens,
     xa, xs = x, None
     if quant_acts:
         xa, xs = per_token_group_quant_fp8(x, 128)
-    act = torch.empty(slots, N, dtype=torch.bfloat16, device=dev)
-    check(L.fmoe_gemm1(wtype, ptr(xa), ptr(xs), ptr(w13), ptr(w13_scale), ptr(w13_zp), K, N,
-                       ctypes.byref(r), int(apply_router_weight_on_input), ptr(act), 0, st), "gemm1")
-    a2, a2s = act, None
+    act_buf = torch.empty(slots, N, dtype=torch.bfloat16, device=dev)
+    ep = _lib.Epilogue(act, ptr(b13), float(alpha), float(limit))
+    check(L.fmoe_gemm1_ex(wtype, ptr(xa), ptr(xs), ptr(w13), ptr(w13_scale), ptr(w13_zp), K, N,
+                          ctypes.byref(r), int(apply_router_weight_on_input), ctypes.byref(ep),
+                          ptr(act_buf), 0, st), "gemm1")
+    a2, a2s = act_buf, None
     if quant_acts:
-        a2, a2s = per_token_group_quant_fp8(act, 128)
+        a2, a2s = per_token_group_quant_fp8(act_buf, 128)
     splits = L.fmoe_gemm2_splits(wtype, K, N, ctypes.byref(r), 0)
     y = torch.empty(splits, slots, K, dtype=torch.float32, device=dev)
-    check(L.fmoe_gemm2(wtype, ptr(a2), ptr(a2s), ptr(w2), ptr(w2_scale), ptr(w2_zp), K, N,
-                       ctypes.byref(r), int(not apply_router_weight_on_input), ptr(y), splits, 0, st),
-          "gemm2")
+    check(L.fmoe_gemm2_ex(wtype, ptr(a2), ptr(a2s), ptr(w2), ptr(w2_scale), ptr(w2_zp), K, N,
+                          ctypes.byref(r), int(not apply_router_weight_on_input), ptr(b2), ptr(y),
+                          splits, 0, st), "gemm2")
     if not combine:
         # per-slot rows, token-major (each token's experts ascending)
         yy = y.sum(0) if splits > 1 else y[0]
@@ -361,8 +376,7 @@ def triton_kernel_fused_experts(
         assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
     assert hidden_states.shape[-1] == w1.shape[-2], "hidden size mismatch"
     assert w2.shape[-1] == w1.shape[1], "intermediate size mismatch"
-    if activation != "silu":
-        raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+    act = _act_code(activation)
     wtype = _wtype_and_check(use_fp8_w8a8, False, w1, w2, w1_scale, w2_scale, None, None,
                              block_shape, per_channel_quant)
     require_cuda(hidden_states, w1, w2)
@@ -382,12 +396,71 @@ def triton_kernel_fused_experts(
     gate_scal = routing_data.gate_scal.float().contiguous()
     return _run_stages(x, w13, w2t, wtype, s13, s2, None, None, M, k, E, topk_indx, gate_indx,
                        gate_scal, offs_raw, offs_pad, tile_map, n_tiles, bm,
-                       apply_router_weight_on_input, 1.0, combine=scatter_indx is not None)
+                       apply_router_weight_on_input, 1.0, combine=scatter_indx is not None, act=act)
 
 
-def triton_kernel_fused_experts_with_bias(*args, **kwargs):
-    """gpt-oss style bias + swiglu variant (ops/fused_moe.py:219-309): not built."""
-    raise AssertionError(_UNSUPPORTED_FEATURE_MSG.format(name="fused experts with bias"))
+def triton_kernel_fused_experts_with_bias(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    w1_pcg,
+    b1: torch.Tensor,
+    w2: torch.Tensor,
+    w2_pcg,
+    b2: torch.Tensor,
+    routing_data,
+    gather_indx,
+    scatter_indx,
+    inplace: bool = False,
+    activation: str = "silu",
+    apply_router_weight_on_input: bool = False,
+    global_num_experts: int = -1,
+    gemm1_alpha: Optional[float] = None,
+    gemm1_clamp_limit: Optional[float] = None,
+) -> torch.Tensor:
+    """Drop-in for ``triton_kernel_fused_experts_with_bias`` (ops/fused_moe.py:219-309).
+
+    ``w1 [E, K, 2N]`` with interleaved gate / linear columns (gate 2j, linear
+    2j+1), ``b1 [E, 2N]``, ``w2 [E, N, K]``, ``b2 [E, K]``; ``activation="silu"``
+    selects the fused swiglu of the reference (:258-259):
+    ``g = min(x_2j + b, limit)``, ``l = clamp(x_2j+1 + b, -limit, limit)``,
+    ``act = g * sigmoid(alpha * g) * (l + 1)`` on the fp32 GEMM1 result, then
+    the routing weight when applied on the input; GEMM2 adds ``b2`` before the
+    routing weight.  ``gemm1_alpha=None`` means 1, ``gemm1_clamp_limit=None`` no
+    clamp.  Only bf16 weights (``w1_pcg`` / ``w2_pcg`` None).
+    """
+    logger.debug("FLAGGEMS_SGLANG FUSED_MOE_WITH_BIAS")
+    assert inplace is False, "Inplace is not supported"
+    assert hidden_states.dtype == torch.bfloat16, "hidden_states must be bfloat16"
+    if activation != "silu":
+        raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+    assert w1_pcg is None, _UNSUPPORTED_FEATURE_MSG.format(name="w1_pcg")
+    assert w2_pcg is None, _UNSUPPORTED_FEATURE_MSG.format(name="w2_pcg")
+    assert hidden_states.ndim == 2, "hidden_states must be 2D"
+    assert w1.dtype == torch.bfloat16, "w1 must be bfloat16"
+    assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
+    assert hidden_states.shape[-1] == w1.shape[-2], "hidden size mismatch"
+    assert w2.shape[-1] == w1.shape[1], "intermediate size mismatch"
+    assert b1 is not None and b2 is not None, "Bias execution requires both w13_bias and w2_bias"
+    E = routing_data.n_expts_tot
+    assert tuple(b1.shape) == (E, w1.shape[2]) and tuple(b2.shape) == (E, w2.shape[2]), \
+        "bias shape mismatch"
+    require_cuda(hidden_states, w1, w2, b1, b2)
+    x = hidden_states.contiguous()
+    M = x.shape[0]
+    k = routing_data.n_expts_act
+    w13 = _as_sglang_layout(w1)
+    w2t = _as_sglang_layout(w2)
+    bm = lib().fmoe_choose_block_m(_lib.W_BF16, M, k, E, 0)
+    offs_raw, offs_pad, tile_map, n_tiles = _expt_data_for(routing_data, M * k, bm)
+    topk_indx = gather_indx.src_indx.to(torch.int32).contiguous()
+    gate_indx = gather_indx.dst_indx.to(torch.int32).contiguous()
+    gate_scal = routing_data.gate_scal.float().contiguous()
+    return _run_stages(x, w13, w2t, _lib.W_BF16, None, None, None, None, M, k, E, topk_indx,
+                       gate_indx, gate_scal, offs_raw, offs_pad, tile_map, n_tiles, bm,
+                       apply_router_weight_on_input, 1.0, combine=scatter_indx is not None,
+                       act=_lib.ACT_SWIGLU, b13=b1.float().contiguous(), b2=b2.float().contiguous(),
+                       alpha=1.0 if gemm1_alpha is None else float(gemm1_alpha),
+                       limit=0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit))
 
 
 # ---------------------------------------------------------------------------
@@ -434,8 +507,7 @@ def fused_experts(
     assert inplace is False, "Inplace is not supported"
     assert a1_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="a1_scale")
     assert a2_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="a2_scale")
-    if activation != "silu":
-        raise ValueError(f"Unsupported FusedMoe activation: {activation}")
+    act = _act_code(activation)
     assert hidden_states.ndim == 2 and hidden_states.dtype == torch.bfloat16, \
         "hidden_states must be 2D bfloat16"
     wtype = _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w1_zp,
@@ -456,14 +528,15 @@ def fused_experts(
         a = _align(topk_weights, topk_ids, E, lib().fmoe_choose_block_m(wtype, M, k, E, path), False)
         return _run_stages(x, w1, w2, wtype, w1_scale, w2_scale, w1_zp, w2_zp, M, k, E,
                            a.topk_indx, a.gate_indx, a.gate_scal, a.offs_raw, a.offs_pad, a.tile_map,
-                           a.n_tiles, a.block_m, apply_router_weight_on_input, 1.0, combine=False)
+                           a.n_tiles, a.block_m, apply_router_weight_on_input, 1.0, combine=False,
+                           act=act)
     ids = _ids_i32(topk_ids)
     tw = topk_weights.float().contiguous()
     out = torch.empty(M, K, dtype=torch.bfloat16, device=x.device)
     args = _lib.FusedArgs(
         wtype, ptr(x), M, K, N, E, k, ptr(w1), ptr(w2), ptr(w1_scale), ptr(w2_scale), ptr(w1_zp),
         ptr(w2_zp), 128, ptr(tw), ptr(ids), int(apply_router_weight_on_input), scale, path,
-        ptr(out), None, 0)
+        ptr(out), None, 0, act, None, None, 1.0, 0.0)
     L = lib()
     nbytes = L.fmoe_fused_experts_workspace_bytes(ctypes.byref(args))
     if nbytes == 0:
@@ -491,7 +564,8 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
 
     Reads the same fields: ``layer.w13_weight [E, 2N, K]`` and
     ``layer.w2_weight [E, K, N]`` (used in place, no per-call transpose),
-    optional ``w13_weight_bias``/``w2_weight_bias`` (bias path: not built),
+    optional ``w13_weight_bias``/``w2_weight_bias`` (bias path, fused swiglu with
+    ``gemm1_alpha`` / ``gemm1_clamp_limit`` from the config),
     ``dispatch_output.hidden_states`` and ``.topk_output`` (either
     ``topk_weights``/``topk_ids`` or a triton_kernels-format
     ``(routing_data, gather_indx, scatter_indx)`` triple), and
@@ -501,8 +575,8 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
     int4 layers ``w13_qweight``/``w13_scales``/``w13_qzeros`` and the w2 ones.
     """
     cfg = obj.runner.config
-    if getattr(layer, "w13_weight_bias", None) is not None or getattr(layer, "w2_weight_bias", None) is not None:
-        raise AssertionError(_UNSUPPORTED_FEATURE_MSG.format(name="fused experts with bias"))
+    b13 = getattr(layer, "w13_weight_bias", None)
+    b2 = getattr(layer, "w2_weight_bias", None)
     hidden_states = dispatch_output.hidden_states
     topk_output = dispatch_output.topk_output
     no_combine = bool(getattr(cfg, "no_combine", False))
@@ -523,7 +597,23 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
         quant = {}
         w13, w2 = layer.w13_weight, layer.w2_weight
 
-    if isinstance(topk_output, tuple) and len(topk_output) == 3 and isinstance(topk_output[0], RoutingData):
+    if b13 is not None or b2 is not None:
+        # bias path (ops/fused_moe.py:364-383): fused swiglu, bf16 weights
+        assert b13 is not None and b2 is not None, "Bias execution requires both w13_bias and w2_bias"
+        assert not quant, _UNSUPPORTED_FEATURE_MSG.format(name="quantized weights with bias")
+        if isinstance(topk_output, tuple) and len(topk_output) == 3 and isinstance(topk_output[0], RoutingData):
+            routing_data, gather_indx, scatter_indx = topk_output
+        else:
+            routing_data, gather_indx, scatter_indx = _standard_topk_to_triton_kernels(
+                topk_output.topk_weights, topk_output.topk_ids, cfg.num_experts)
+        out = triton_kernel_fused_experts_with_bias(
+            hidden_states, w13.transpose(-1, -2), None, b13, w2.transpose(-1, -2), None, b2,
+            routing_data, gather_indx, None if no_combine else scatter_indx, activation=activation,
+            apply_router_weight_on_input=on_input, gemm1_alpha=getattr(cfg, "gemm1_alpha", None),
+            gemm1_clamp_limit=getattr(cfg, "gemm1_clamp_limit", None))
+        if scale is not None:
+            out.mul_(scale)
+    elif isinstance(topk_output, tuple) and len(topk_output) == 3 and isinstance(topk_output[0], RoutingData):
         routing_data, gather_indx, scatter_indx = topk_output
         assert not quant.get("use_int4_w4a16"), _UNSUPPORTED_FEATURE_MSG.format(
             name="int4 with triton_kernels routing")

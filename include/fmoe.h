@@ -48,6 +48,14 @@ enum fmoe_wtype {
   FMOE_W_INT4 = 2,     /* uint4 weights with fp16 group scales and uint4 zeros, bf16 activations */
 };
 
+/* GEMM1 activations (the fused epilogue of fmoe_gemm1_ex / fmoe_fused_experts). */
+enum fmoe_activation {
+  FMOE_ACT_SILU = 0,   /* silu(gate) * up, gate rows 0..N-1, up rows N..2N-1 (ops/fused_moe.py:28-47) */
+  FMOE_ACT_GELU = 1,   /* gelu(gate) * up with the exact (erf) GELU, same split (ops/fused_moe.py:203-204) */
+  FMOE_ACT_SWIGLU = 2, /* swiglu of the bias path (ops/fused_moe.py:258-259): rows interleaved,
+                          gate = row 2j, linear = row 2j+1; see fmoe_epilogue */
+};
+
 /* Text of a status code, and the message of the last failure on this thread. */
 const char* fmoe_status_string(int status);
 const char* fmoe_last_error(void);
@@ -186,6 +194,37 @@ int fmoe_gemm2(int wtype, const void* act, const float* act_scale, const void* w
                void* stream);
 int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_routing* r, int path);
 
+/* Epilogue options of the bias / activation variants
+ * (triton_kernel_fused_experts_with_bias, ops/fused_moe.py:219-309, and the
+ * gelu branch of triton_kernel_fused_experts, :203-204).
+ *   activation: enum fmoe_activation.
+ *   bias: fp32 [E, rows] added to the fp32 GEMM result (GEMM1 rows = 2N in
+ *     w13 row order, GEMM2 rows = K), or null.  With GEMM2 split-K the bias
+ *     is added to split 0 only.
+ *   alpha, limit (SWIGLU): with g = gate + b, l = linear + b, and when
+ *     limit > 0: g = min(g, limit), l = clamp(l, -limit, limit);
+ *     act = g * sigmoid(alpha * g) * (l + 1).  The routing weight (when
+ *     applied on the input) multiplies the activation output.
+ *   SILU / GELU round the GEMM1 result to bf16 before the activation (the
+ *   reference runs them as a separate pass over a bf16 tensor); SWIGLU works
+ *   on the fp32 result (the reference fuses it into matmul_ogs). */
+typedef struct fmoe_epilogue {
+  int32_t activation;
+  const float* bias;
+  float alpha;
+  float limit;
+} fmoe_epilogue;
+
+/* fmoe_gemm1 / fmoe_gemm2 with an epilogue (null = SiLU, no bias). */
+int fmoe_gemm1_ex(int wtype, const void* x, const float* x_scale, const void* w13,
+                  const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
+                  const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep, void* act,
+                  int path, void* stream);
+int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale, const void* w2,
+                  const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
+                  const fmoe_routing* r, int apply_gamma, const float* bias, float* y, int splits,
+                  int path, void* stream);
+
 /* Tile height the library pairs with the GEMM kernels for a problem size:
  * 16 selects the decode (streaming) kernels, 64 / 128 / 256 the prefill kernels.
  * path: 0 = choose, 1 = prefill, 2 = decode (int4 is decode-only). */
@@ -225,6 +264,12 @@ typedef struct fmoe_fused_args {
   void* out;
   void* workspace;
   size_t workspace_bytes;
+  /* ABI version 2: epilogue of the bias / activation variants */
+  int32_t activation;  /* enum fmoe_activation */
+  const float* b13;    /* fp32 [E, 2N] or null */
+  const float* b2;     /* fp32 [E, K] or null */
+  float alpha;         /* SWIGLU */
+  float limit;         /* SWIGLU clamp, <= 0 = none */
 } fmoe_fused_args;
 
 size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a);

@@ -33,8 +33,24 @@ compute_expt_data              brute-force loops + invariants.  The encoding
                                *parity to triton_kernels unpinned*.
 moe_align_block_size           brute-force loops + invariants (SGLang format)
 silu_and_mul                   scipy ``expit`` closed form
+gelu_and_mul                   ``torch.nn.functional.gelu`` (exact erf form,
+                               library routine); Phi(1) known value; the
+                               identity gelu(x) - gelu(-x) = x.  The routine is
+                               sgl_kernel's ``gelu_and_mul`` (external).
+swiglu                         reduces to ``torch.nn.functional.silu`` for
+                               alpha = 1, no clamp, linear = 0; clamp and
+                               interleaving checked against closed forms.  The
+                               routine is triton_kernels' ``swiglu_fn``
+                               (external, absent): *parity unpinned* (alpha /
+                               limit / the +1 on the linear half follow the
+                               published gpt-oss swiglu).
 fused_experts (bf16)           fp64 per-token brute force; E=1/k=1 reduces to
-                               a dense SwiGLU MLP (textbook routine)
+                               a dense SwiGLU MLP (textbook routine); gelu
+                               variant: E=1/k=1 dense GeGLU with torch's gelu
+fused_experts_bias             fp64 per-token brute force; zero weights reduce
+                               to sum_j w_j b2[e_j] (closed form).  The order
+                               bias -> activation -> routing weight inside
+                               matmul_ogs is *unpinned* (external code).
 per_token_group_quant_fp8      torch ``float8_e4m3fn`` cast; exact powers of 2;
                                amax element maps to +-448 exactly
 block_quant_fp8                same; dequant round-trip error bound
@@ -240,6 +256,30 @@ def silu_and_mul(inter: torch.Tensor) -> torch.Tensor:
     return (g / (1.0 + torch.exp(-g))) * u
 
 
+def gelu_and_mul(inter: torch.Tensor) -> torch.Tensor:
+    """``gelu_and_mul`` (sgl_kernel, called at ``ops/fused_moe.py:19-21,203-204``):
+    gate = first half, up = second half, exact (erf) GELU of the gate times
+    up, in fp32."""
+    h = inter.shape[-1] // 2
+    g = inter[..., :h].double()
+    u = inter[..., h:].double()
+    erf = torch.special.erf(g / np.sqrt(2.0))
+    return (0.5 * g * (1.0 + erf) * u).float()
+
+
+def swiglu(inter: torch.Tensor, alpha: float = 1.0, limit: float | None = None) -> torch.Tensor:
+    """The fused activation of the bias path (``ops/fused_moe.py:258-259``,
+    triton_kernels ``swiglu_fn``): columns interleaved, gate = even, linear =
+    odd; ``g = min(gate, limit)``, ``l = clamp(linear, -limit, limit)`` when a
+    limit is given; ``g * sigmoid(alpha * g) * (l + 1)`` in fp32."""
+    g = inter[..., 0::2].double()
+    lin = inter[..., 1::2].double()
+    if limit is not None and limit > 0:
+        g = torch.clamp(g, max=limit)
+        lin = torch.clamp(lin, min=-limit, max=limit)
+    return (g / (1.0 + torch.exp(-alpha * g)) * (lin + 1.0)).float()
+
+
 # --------------------------------------------------------------------------
 # fused experts (bf16 semantics)
 # --------------------------------------------------------------------------
@@ -266,6 +306,7 @@ def fused_experts(
     w2_deq=None,
     act_quant=None,
     a1_deq=None,
+    activation: str = "silu",
 ):
     """Fused MoE forward, ``triton_kernel_fused_experts`` (``ops/fused_moe.py:181-216``).
 
@@ -282,7 +323,10 @@ def fused_experts(
 
     ``w13_deq``/``w2_deq`` (callables e -> fp32 matrix) and ``act_quant`` /
     ``a1_deq`` let the fp8 / int4 oracles reuse this with dequantized operands.
+    ``activation``: "silu" (``_silu_and_mul_triton``) or "gelu"
+    (``gelu_and_mul``), the branch at :198-206.
     """
+    act_fn = {"silu": silu_and_mul, "gelu": gelu_and_mul}[activation]
     M, K = x.shape
     k = topk_ids.shape[1]
     E = w13.shape[0] if w13 is not None else w13_deq.E
@@ -298,7 +342,7 @@ def fused_experts(
         if apply_router_weight_on_input:
             inter = inter * gate_scal[a:b, None]
         inter = inter.to(torch.bfloat16)
-        act = silu_and_mul(inter).to(torch.bfloat16).float()
+        act = act_fn(inter).to(torch.bfloat16).float()
         if act_quant is not None:
             act = act_quant(act)
         out = act @ W2.t()
@@ -310,6 +354,58 @@ def fused_experts(
     if routed_scaling_factor is not None and routed_scaling_factor != 1.0:
         res = res * routed_scaling_factor
     return res.to(torch.bfloat16)
+
+
+def fused_experts_bias(x, w13, b13, w2, b2, topk_weights, topk_ids,
+                       apply_router_weight_on_input: bool = False, alpha: float = 1.0,
+                       limit: float | None = None):
+    """``triton_kernel_fused_experts_with_bias`` (``ops/fused_moe.py:219-309``),
+    SGLang layouts ``w13 [E, 2N, K]`` with interleaved gate / linear rows,
+    ``b13 [E, 2N]``, ``w2 [E, K, N]``, ``b2 [E, K]``.  GEMM1 (fp32 accumulate)
+    + bias -> swiglu in fp32 (fused into matmul_ogs, no bf16 rounding of the
+    GEMM1 result) -> routing weight when applied on the input -> bf16; GEMM2
+    (fp32) + bias -> routing weight otherwise; top-k sum in fp32 -> bf16."""
+    M, K = x.shape
+    k = topk_ids.shape[1]
+    E = w13.shape[0]
+    r = standard_topk_to_routing(topk_weights, topk_ids, E)
+    xin = x.float()
+    y = torch.zeros(M * k, K, dtype=torch.float32)
+    gate_scal = torch.from_numpy(r["gate_scal"])
+    for e, a, b, tok in _expert_groups(r, k):
+        tok = torch.from_numpy(tok.astype(np.int64))
+        inter = xin[tok] @ w13[e].float().t() + b13[e].float()
+        act = swiglu(inter, alpha, limit)
+        if apply_router_weight_on_input:
+            act = act * gate_scal[a:b, None]
+        act = act.to(torch.bfloat16).float()
+        out = act @ w2[e].float().t() + b2[e].float()
+        if not apply_router_weight_on_input:
+            out = out * gate_scal[a:b, None]
+        flat = torch.from_numpy(r["topk_indx"][a:b].astype(np.int64))
+        y[flat] = out
+    return y.view(M, k, K).sum(dim=1).to(torch.bfloat16)
+
+
+def fused_experts_bias_bruteforce(x, w13, b13, w2, b2, topk_weights, topk_ids, alpha=1.0,
+                                  limit=None):
+    """Second oracle for the bias path: per-token, per-slot loop in fp64."""
+    M, K = x.shape
+    N = w2.shape[2]
+    xd = x.double()
+    out = torch.zeros(M, K, dtype=torch.float64)
+    for t in range(M):
+        for j in range(topk_ids.shape[1]):
+            e = int(topk_ids[t, j])
+            h = w13[e].double() @ xd[t] + b13[e].double()
+            g, lin = h[0::2], h[1::2]
+            if limit is not None and limit > 0:
+                g = g.clamp(max=limit)
+                lin = lin.clamp(-limit, limit)
+            a = g * torch.sigmoid(alpha * g) * (lin + 1.0)
+            out[t] += float(topk_weights[t, j]) * (w2[e].double() @ a + b2[e].double())
+    assert out.shape[1] == K and N * 2 == w13.shape[1]
+    return out
 
 
 def fused_experts_bruteforce(x, w13, w2, topk_weights, topk_ids):

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_queries():
     L = _lib.lib()
-    assert L.fmoe_abi_version() == 1
+    assert L.fmoe_abi_version() == 2
     assert L.fmoe_status_string(2) == b"not supported"
     assert L.fmoe_max_tiles(8, 256) == 8
     assert L.fmoe_max_tiles(65536, 256) == 255 + (65536 - 256 + 1 + 15) // 16

@@ -205,3 +205,53 @@ def test_mixtral_prefill_permutation_and_determinism():
     ids_l = ids.clone().apply_(lambda e: remap[e])
     ref = O.fused_experts(xs, w13[used].cpu(), w2[used].cpu(), ws, ids_l)
     _close(a[sel.to(DEV)], ref, 2e-2)
+
+
+# ------------------------------------------------------------ activations / bias path
+@pytest.mark.parametrize("path", [1, 2])
+@pytest.mark.parametrize("M", [1, 64, 300])
+def test_gelu_activation(M, path):
+    """activation="gelu" (ops/fused_moe.py:203-204) on both kernel families."""
+    K, N, E, k = 512, 384, 16, 4
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), d["w13"].to(DEV), d["w2"].to(DEV),
+                                        d["topk_weights"].to(DEV), d["topk_ids"].to(DEV), path=path,
+                                        activation="gelu")
+    ref = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"],
+                          activation="gelu")
+    _close(out, ref, 2e-2)
+
+
+@pytest.mark.parametrize("shape", FUSED_MOE_SHAPES_SMALL, ids=lambda s: "M{}_K{}_N{}_E{}_topk{}".format(*s))
+def test_gelu_reference_api(shape):
+    M, K, N, E, topk = shape
+    x, w1, w2, tw, ti = _ref_inputs(M, K, N, E, topk)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw.to(DEV), ti.to(DEV), E)
+    res = flaggems_sglang.triton_kernel_fused_experts(x.to(DEV), w1.to(DEV), w2.to(DEV), rd, gi, si,
+                                                      activation="gelu")
+    ref = O.fused_experts(x, w1.transpose(1, 2), w2.transpose(1, 2), tw, ti, activation="gelu")
+    _close(res, ref, 2e-2)
+
+
+@pytest.mark.parametrize("on_input", [False, True])
+@pytest.mark.parametrize("alpha,limit", [(None, None), (1.702, 7.0), (1.0, 0.05)])
+@pytest.mark.parametrize("M", [1, 16, 200])
+def test_bias_swiglu(M, alpha, limit, on_input):
+    """triton_kernel_fused_experts_with_bias (ops/fused_moe.py:219-309): biases,
+    interleaved swiglu with alpha / clamp limit, both routing-weight placements,
+    decode (M <= 16) and prefill kernels."""
+    K, N, E, k = 256, 384, 8, 2
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    gen = torch.Generator().manual_seed(M + 3)
+    b13 = torch.randn(E, 2 * N, generator=gen) * 0.1
+    b2 = torch.randn(E, K, generator=gen) * 0.1
+    rd, gi, si = F._standard_topk_to_triton_kernels(d["topk_weights"].to(DEV), d["topk_ids"].to(DEV), E)
+    w1 = d["w13"].transpose(1, 2).to(DEV)          # matmul_ogs layout [E, K, 2N], interleaved columns
+    w2 = d["w2"].transpose(1, 2).to(DEV)           # [E, N, K]
+    out = flaggems_sglang.triton_kernel_fused_experts_with_bias(
+        d["x"].to(DEV), w1, None, b13.to(DEV), w2, None, b2.to(DEV), rd, gi, si,
+        apply_router_weight_on_input=on_input, gemm1_alpha=alpha, gemm1_clamp_limit=limit)
+    ref = O.fused_experts_bias(d["x"], d["w13"], b13, d["w2"], b2, d["topk_weights"], d["topk_ids"],
+                               apply_router_weight_on_input=on_input,
+                               alpha=1.0 if alpha is None else alpha, limit=limit)
+    _close(out, ref, 2e-2)

@@ -57,6 +57,39 @@ def test_cpu_tensors_are_rejected_not_computed():
         flaggems_sglang.fused_experts(x, w1, w2, torch.ones(2, 2), torch.zeros(2, 2, dtype=torch.int32))
 
 
-def test_bias_path_not_built():
-    with pytest.raises(AssertionError, match="is not supported"):
-        flaggems_sglang.triton_kernel_fused_experts_with_bias()
+def test_bias_path_argument_checks():
+    """triton_kernel_fused_experts_with_bias (ops/fused_moe.py:219-309): the
+    reference's asserts and its ValueError for other activations, raised
+    before any device work (host tensors are enough)."""
+    E, K, N, M = 4, 128, 128, 3
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    w1 = torch.zeros(E, K, 2 * N, dtype=torch.bfloat16)
+    w2 = torch.zeros(E, N, K, dtype=torch.bfloat16)
+    b1 = torch.zeros(E, 2 * N)
+    b2 = torch.zeros(E, K)
+    rd = F.RoutingData(torch.ones(M * 2), torch.zeros(E, dtype=torch.int32), E, 2, None)
+    f = flaggems_sglang.triton_kernel_fused_experts_with_bias
+    with pytest.raises(AssertionError, match="Inplace is not supported"):
+        f(x, w1, None, b1, w2, None, b2, rd, None, None, inplace=True)
+    with pytest.raises(ValueError, match="Unsupported FusedMoe activation: gelu"):
+        f(x, w1, None, b1, w2, None, b2, rd, None, None, activation="gelu")
+    with pytest.raises(AssertionError, match="w1_pcg is not supported"):
+        f(x, w1, object(), b1, w2, None, b2, rd, None, None)
+    with pytest.raises(AssertionError, match="requires both"):
+        f(x, w1, None, b1, w2, None, None, rd, None, None)
+    with pytest.raises(ValueError, match="GPU"):
+        f(x, w1, None, b1, w2, None, b2, rd, None, None)
+
+
+def test_activation_names():
+    """silu and gelu are accepted (ops/fused_moe.py:198-206); anything else is
+    the reference's ValueError."""
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    w1 = torch.zeros(8, 512, 128, dtype=torch.bfloat16)
+    w2 = torch.zeros(8, 128, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="Unsupported FusedMoe activation: relu"):
+        flaggems_sglang.fused_experts(x, w1, w2, torch.ones(2, 2), torch.zeros(2, 2, dtype=torch.int32),
+                                      activation="relu")
+    with pytest.raises(ValueError, match="GPU"):
+        flaggems_sglang.fused_experts(x, w1, w2, torch.ones(2, 2), torch.zeros(2, 2, dtype=torch.int32),
+                                      activation="gelu")

@@ -334,3 +334,74 @@ def test_int4_quant_error_bound():
         d = O.dequant_int4(qw[e], sc[e], z[e])
         s = sc[e].float().t().repeat_interleave(128, 1)
         assert torch.all((d - w[e]).abs() <= s * 0.5 + s * 2e-3)
+
+
+# ------------------------------------------------------------ activations / bias path
+def test_gelu_and_mul_library_and_known_values():
+    g = torch.linspace(-6, 6, 241)
+    u = torch.linspace(-2, 3, 241)
+    got = O.gelu_and_mul(torch.cat([g, u]).view(1, -1))[0]
+    ref = torch.nn.functional.gelu(g.double(), approximate="none") * u.double()
+    assert torch.allclose(got.double(), ref, atol=1e-6, rtol=1e-6)
+    one = O.gelu_and_mul(torch.tensor([[1.0, 1.0]]))[0, 0].item()
+    assert abs(one - 0.8413447460685429) < 1e-6          # Phi(1)
+    x = torch.linspace(-4, 4, 81)
+    pos = O.gelu_and_mul(torch.cat([x, torch.ones(81)]).view(1, -1))[0]
+    neg = O.gelu_and_mul(torch.cat([-x, torch.ones(81)]).view(1, -1))[0]
+    assert torch.allclose(pos - neg, x, atol=1e-6)        # gelu(x) - gelu(-x) = x
+
+
+def test_swiglu_reduces_to_silu_and_clamps():
+    g = torch.linspace(-8, 8, 161)
+    inter = torch.zeros(1, 2 * g.numel())
+    inter[0, 0::2] = g                                    # gate even, linear odd (= 0)
+    got = O.swiglu(inter, alpha=1.0, limit=None)[0]
+    assert torch.allclose(got, torch.nn.functional.silu(g), atol=1e-6)
+    a, lim = 1.702, 7.0
+    inter = torch.tensor([[10.0, 10.0, 10.0, -10.0, -3.0, 2.0]])
+    got = O.swiglu(inter, alpha=a, limit=lim)[0]
+    sig = lambda z: 1.0 / (1.0 + math.exp(-z))           # noqa: E731
+    want = [lim * sig(a * lim) * (lim + 1), lim * sig(a * lim) * (-lim + 1), -3 * sig(-3 * a) * 3]
+    assert torch.allclose(got.double(), torch.tensor(want, dtype=torch.float64), rtol=1e-6)
+
+
+def test_fused_experts_gelu_dense_geglu():
+    """E=1, k=1 with weight 1: the MoE is a dense GeGLU MLP with the same
+    rounding points, written with torch's gelu (library routine)."""
+    d = O.make_inputs(9, 64, 32, 1, 1, wscale=0.2)
+    tw = torch.ones(9, 1)
+    got = O.fused_experts(d["x"], d["w13"], d["w2"], tw, d["topk_ids"], activation="gelu")
+    w13, w2 = d["w13"][0].float(), d["w2"][0].float()
+    inter = (d["x"].float() @ w13.t()).to(torch.bfloat16).float()
+    g, u = inter[:, :32], inter[:, 32:]
+    act = (torch.nn.functional.gelu(g) * u).to(torch.bfloat16).float()
+    ref = (act @ w2.t()).to(torch.bfloat16)
+    assert torch.allclose(got.float(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
+def test_fused_experts_bias_matches_bruteforce():
+    d = O.make_inputs(13, 128, 64, 6, 2, wscale=0.1)
+    gen = torch.Generator().manual_seed(5)
+    b13 = torch.randn(6, 128, generator=gen) * 0.2
+    b2 = torch.randn(6, 128, generator=gen) * 0.2
+    for alpha, limit in ((1.0, None), (1.702, 0.5)):
+        got = O.fused_experts_bias(d["x"], d["w13"], b13, d["w2"], b2, d["topk_weights"],
+                                   d["topk_ids"], alpha=alpha, limit=limit)
+        ref = O.fused_experts_bias_bruteforce(d["x"], d["w13"], b13, d["w2"], b2, d["topk_weights"],
+                                              d["topk_ids"], alpha=alpha, limit=limit)
+        err = (got.double() - ref).abs().max().item()
+        assert err < 2e-2 * max(1.0, ref.abs().max().item()), err
+
+
+def test_fused_experts_bias_zero_weights_closed_form():
+    """Zero weights: every slot's output is its expert's b2, so the MoE
+    returns sum_j w_j * b2[e_j]."""
+    d = O.make_inputs(7, 128, 64, 5, 3, wscale=0.1)
+    gen = torch.Generator().manual_seed(9)
+    b13 = torch.randn(5, 128, generator=gen)
+    b2 = torch.randn(5, 128, generator=gen)
+    z13 = torch.zeros_like(d["w13"])
+    z2 = torch.zeros_like(d["w2"])
+    got = O.fused_experts_bias(d["x"], z13, b13, z2, b2, d["topk_weights"], d["topk_ids"])
+    want = (d["topk_weights"][..., None] * b2[d["topk_ids"].long()]).sum(1)
+    assert torch.allclose(got.float(), want, atol=1e-2, rtol=1e-2)
