@@ -36,7 +36,17 @@ struct AlignParams {
   int32_t* chunk_base;  // [n_chunks, E]
   int32_t* sort_col;    // [M*k] original column of each row-sorted entry
   fmoe_align_out o;
+  const int32_t* emap;  // optional expert map: global id -> local id or -1
+  int n_global;
 };
+
+// Expert id of flat slot f (global -> local through the expert map, if any;
+// ids outside the map, or mapped to -1, are dropped like out-of-range ids).
+__device__ __forceinline__ int load_id(const AlignParams& p, int64_t f) {
+  int v = p.ids[f];
+  if (p.emap) v = (v >= 0 && v < p.n_global) ? p.emap[v] : -1;
+  return v;
+}
 
 // ---- phase 1: per-token sort + chunk histogram
 __device__ void phase_rows(const AlignParams& p, int c, int* h) {
@@ -45,13 +55,12 @@ __device__ void phase_rows(const AlignParams& p, int c, int* h) {
   __syncthreads();
   const int64_t t = static_cast<int64_t>(c) * kAlignThreads + tid;
   if (t < p.M) {
-    const int32_t* row = p.ids + t * p.k;
     const float* wr = p.w + t * p.k;
     for (int j = 0; j < p.k; ++j) {
-      int idj = row[j];
+      int idj = load_id(p, t * p.k + j);
       int rank = 0;
       for (int i = 0; i < p.k; ++i) {
-        int idi = row[i];
+        int idi = load_id(p, t * p.k + i);
         rank += (idi < idj) || (idi == idj && i < j);
       }
       int64_t f = t * p.k + rank;
@@ -291,7 +300,7 @@ __global__ __launch_bounds__(kAlignThreads) void align_tiny_kernel(AlignParams p
     for (int w = 0; w < kAlignThreads / kWave; ++w) wcnt[w][e] = 0;
   }
   for (int f = tid; f < n; f += kAlignThreads) {  // coalesced, independent loads
-    s_id[f] = p.ids[f];
+    s_id[f] = load_id(p, f);
     s_w[f] = p.w[f];
   }
   __syncthreads();
@@ -423,7 +432,17 @@ extern "C" size_t fmoe_align_workspace_bytes(int64_t M, int k, int E) {
 extern "C" int fmoe_align(const int32_t* topk_ids, const float* topk_weights, int64_t M, int k,
                           int E, int block_m, const fmoe_align_out* out, void* workspace,
                           size_t workspace_bytes, void* stream) {
+  return fmoe_align_ex(topk_ids, topk_weights, M, k, E, block_m, nullptr, 0, out, workspace,
+                       workspace_bytes, stream);
+}
+
+extern "C" int fmoe_align_ex(const int32_t* topk_ids, const float* topk_weights, int64_t M, int k,
+                             int E, int block_m, const int32_t* expert_map, int n_global,
+                             const fmoe_align_out* out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   if (!out) return fail(FMOE_ERR_INVALID, "align: null output struct");
+  if (expert_map && n_global < 1)
+    return fail(FMOE_ERR_INVALID, "align: expert map needs n_global >= 1 (got %d)", n_global);
   if (M < 0 || k < 1 || k > 32 || E < 1 || E > kMaxExperts)
     return fail(FMOE_ERR_INVALID, "align: need 1 <= k <= 32, 1 <= E <= %d (M=%lld k=%d E=%d)",
                 kMaxExperts, static_cast<long long>(M), k, E);
@@ -457,6 +476,8 @@ extern "C" int fmoe_align(const int32_t* topk_ids, const float* topk_weights, in
   p.chunk_base = reinterpret_cast<int32_t*>(ws + align_up(sizeof(int32_t) * C * E));
   p.sort_col = reinterpret_cast<int32_t*>(ws + 2 * align_up(sizeof(int32_t) * C * E));
   p.o = o;
+  p.emap = expert_map;
+  p.n_global = expert_map ? n_global : 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (M * k <= kTinySlots) {
     align_tiny_kernel<<<1, kAlignThreads, 0, s>>>(p);

@@ -329,8 +329,9 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   o.offs_pad = static_cast<int32_t*>(at(L.offs_pad));
   o.tile_map = static_cast<int32_t*>(at(L.tile_map));
   o.n_tiles = static_cast<int32_t*>(at(L.n_tiles));
-  if (int st = fmoe_align(a->topk_ids, a->topk_weights, a->M, a->top_k, a->E, L.bm, &o,
-                          at(L.align_ws), fmoe_align_workspace_bytes(a->M, a->top_k, a->E), stream))
+  if (int st = fmoe_align_ex(a->topk_ids, a->topk_weights, a->M, a->top_k, a->E, L.bm,
+                             a->expert_map, a->n_global, &o, at(L.align_ws),
+                             fmoe_align_workspace_bytes(a->M, a->top_k, a->E), stream))
     return st;
 
   fmoe_routing r{};

@@ -59,7 +59,7 @@ class FusedArgs(ctypes.Structure):
         ("apply_router_weight_on_input", ctypes.c_int32), ("routed_scaling_factor", ctypes.c_float),
         ("path", ctypes.c_int32), ("out", vp), ("workspace", vp), ("workspace_bytes", ctypes.c_size_t),
         ("activation", ctypes.c_int32), ("b13", vp), ("b2", vp), ("alpha", ctypes.c_float),
-        ("limit", ctypes.c_float),
+        ("limit", ctypes.c_float), ("expert_map", vp), ("n_global", ctypes.c_int32),
     ]
 
 
@@ -76,6 +76,9 @@ _SIGS = {
     "fmoe_align_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int, ctypes.c_int]),
     "fmoe_align": (ctypes.c_int, [vp, vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                   ctypes.POINTER(AlignOut), vp, ctypes.c_size_t, vp]),
+    "fmoe_align_ex": (ctypes.c_int, [vp, vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     vp, ctypes.c_int, ctypes.POINTER(AlignOut), vp, ctypes.c_size_t,
+                                     vp]),
     "fmoe_expt_data": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_int64, ctypes.c_int, vp, vp, vp, vp, vp]),
     "fmoe_quant_fp8_group": (ctypes.c_int, [vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, vp, vp, vp]),
     "fmoe_gemm1": (ctypes.c_int, [ctypes.c_int, vp, vp, vp, vp, vp, ctypes.c_int64, ctypes.c_int64,

@@ -133,8 +133,9 @@ def _ids_i32(topk_ids: torch.Tensor) -> torch.Tensor:
         topk_ids.to(torch.int32).contiguous()
 
 
-def _align(topk_weights, topk_ids, n_experts: int, block_m: int, sglang_format: bool) -> _Align:
-    require_cuda(topk_weights, topk_ids)
+def _align(topk_weights, topk_ids, n_experts: int, block_m: int, sglang_format: bool,
+           expert_map: Optional[torch.Tensor] = None) -> _Align:
+    require_cuda(topk_weights, topk_ids, expert_map)
     L = lib()
     ids = _ids_i32(topk_ids)
     w = topk_weights.float().contiguous()
@@ -158,8 +159,10 @@ def _align(topk_weights, topk_ids, n_experts: int, block_m: int, sglang_format: 
     o = _lib.AlignOut(*[ptr(getattr(a, f)) for f, _ in _lib.AlignOut._fields_])
     ws_bytes = L.fmoe_align_workspace_bytes(M, k, n_experts)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    check(L.fmoe_align(ptr(ids), ptr(w), M, k, n_experts, block_m, ctypes.byref(o), ptr(ws),
-                       ws_bytes, stream_of(ids)), "moe_align")
+    emap = None if expert_map is None else _ids_i32(expert_map.view(1, -1)).view(-1)
+    check(L.fmoe_align_ex(ptr(ids), ptr(w), M, k, n_experts, block_m, ptr(emap),
+                          0 if emap is None else emap.numel(), ctypes.byref(o), ptr(ws), ws_bytes,
+                          stream_of(ids)), "moe_align")
     return a
 
 
@@ -491,6 +494,8 @@ def fused_experts(
     routed_scaling_factor: Optional[float] = None,
     no_combine: bool = False,
     path: int = 0,
+    expert_map: Optional[torch.Tensor] = None,
+    global_num_experts: int = -1,
 ) -> torch.Tensor:
     """Whole fused MoE in one C call (align -> GEMM1+SiLU -> GEMM2 -> top-k sum).
 
@@ -503,6 +508,10 @@ def fused_experts(
            / ``w2_scale [E, N/128, K]`` fp16, ``w1_zp [E, K/128, N]`` /
            ``w2_zp [E, N/128, K/2]`` uint8 (two uint4 zeros per byte).
     ``path``: 0 choose, 1 prefill kernels, 2 decode kernels.
+    ``expert_map`` (expert parallel): ``topk_ids`` hold global expert ids,
+    ``expert_map [global_num_experts]`` int maps each to a local expert (index
+    into ``w1`` / ``w2``) or -1; choices of non-local experts are dropped, so
+    each token gets the sum over its local experts only.
     """
     assert inplace is False, "Inplace is not supported"
     assert a1_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="a1_scale")
@@ -524,8 +533,15 @@ def fused_experts(
         if t is not None:
             assert t.is_contiguous(), "weights and scales must be contiguous"
     scale = 1.0 if routed_scaling_factor is None else float(routed_scaling_factor)
+    emap = None
+    if expert_map is not None:
+        require_cuda(expert_map)
+        n_global = global_num_experts if global_num_experts > 0 else expert_map.numel()
+        assert expert_map.numel() == n_global, "expert_map must have global_num_experts entries"
+        emap = _ids_i32(expert_map.view(1, -1)).view(-1)
     if no_combine:
-        a = _align(topk_weights, topk_ids, E, lib().fmoe_choose_block_m(wtype, M, k, E, path), False)
+        a = _align(topk_weights, topk_ids, E, lib().fmoe_choose_block_m(wtype, M, k, E, path), False,
+                   expert_map=emap)
         return _run_stages(x, w1, w2, wtype, w1_scale, w2_scale, w1_zp, w2_zp, M, k, E,
                            a.topk_indx, a.gate_indx, a.gate_scal, a.offs_raw, a.offs_pad, a.tile_map,
                            a.n_tiles, a.block_m, apply_router_weight_on_input, 1.0, combine=False,
@@ -536,7 +552,7 @@ def fused_experts(
     args = _lib.FusedArgs(
         wtype, ptr(x), M, K, N, E, k, ptr(w1), ptr(w2), ptr(w1_scale), ptr(w2_scale), ptr(w1_zp),
         ptr(w2_zp), 128, ptr(tw), ptr(ids), int(apply_router_weight_on_input), scale, path,
-        ptr(out), None, 0, act, None, None, 1.0, 0.0)
+        ptr(out), None, 0, act, None, None, 1.0, 0.0, ptr(emap), 0 if emap is None else emap.numel())
     L = lib()
     nbytes = L.fmoe_fused_experts_workspace_bytes(ctypes.byref(args))
     if nbytes == 0:

@@ -137,6 +137,17 @@ int fmoe_align(const int32_t* topk_ids, const float* topk_weights, int64_t M, in
 
 /* ExptData from a histogram alone (compute_expt_data_torch; used when the
  * caller already holds triton_kernels-format routing, ops/fused_moe.py:339-340). */
+/* fmoe_align with an expert map (expert parallel; the reference's
+ * expert_map / global_num_experts arguments, ops/fused_moe.py:145-146,160):
+ * topk_ids hold global ids in [0, n_global); expert_map [n_global] int32 maps
+ * each to a local expert in [0, E) or to -1.  Slots whose expert is not local
+ * are dropped (gate_indx = -1, no GEMM rows; their tokens get contributions
+ * from the local experts only).  expert_map null = identity (fmoe_align). */
+int fmoe_align_ex(const int32_t* topk_ids, const float* topk_weights, int64_t M, int k, int E,
+                  int block_m, const int32_t* expert_map, int n_global,
+                  const fmoe_align_out* out, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
 int fmoe_expt_data(const int32_t* hist, int E, int64_t n_slots, int block_m, int32_t* offs_raw,
                    int32_t* offs_pad, int32_t* tile_map, int32_t* n_tiles, void* stream);
 
@@ -270,6 +281,8 @@ typedef struct fmoe_fused_args {
   const float* b2;     /* fp32 [E, K] or null */
   float alpha;         /* SWIGLU */
   float limit;         /* SWIGLU clamp, <= 0 = none */
+  const int32_t* expert_map; /* [n_global] global -> local expert (or -1), or null */
+  int32_t n_global;          /* global expert count when expert_map is set */
 } fmoe_fused_args;
 
 size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a);

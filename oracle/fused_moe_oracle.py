@@ -47,6 +47,10 @@ swiglu                         reduces to ``torch.nn.functional.silu`` for
 fused_experts (bf16)           fp64 per-token brute force; E=1/k=1 reduces to
                                a dense SwiGLU MLP (textbook routine); gelu
                                variant: E=1/k=1 dense GeGLU with torch's gelu
+ep_localize                    identity map = no map; two ranks with disjoint
+                               maps sum to the single-rank output (the EP
+                               invariant); the map semantics is SGLang's
+                               (external) expert_map: global -> local or -1
 fused_experts_bias             fp64 per-token brute force; zero weights reduce
                                to sum_j w_j b2[e_j] (closed form).  The order
                                bias -> activation -> routing weight inside
@@ -354,6 +358,22 @@ def fused_experts(
     if routed_scaling_factor is not None and routed_scaling_factor != 1.0:
         res = res * routed_scaling_factor
     return res.to(torch.bfloat16)
+
+
+def ep_localize(topk_weights, topk_ids, expert_map):
+    """Expert parallel (the ``expert_map`` / ``global_num_experts`` arguments,
+    ``ops/fused_moe.py:145-146,160``): ``expert_map [n_global]`` maps a global
+    expert id to a local one or -1.  Returns routing for the local experts in
+    which every non-local choice points at local expert 0 with weight 0, so it
+    contributes exactly 0 (silu(0)·0 = 0 also when the weight multiplies the
+    input)."""
+    emap = torch.as_tensor(expert_map).long()
+    ids = torch.as_tensor(topk_ids).long()
+    ok = (ids >= 0) & (ids < emap.numel())
+    loc = torch.where(ok, emap[ids.clamp(0, emap.numel() - 1)], torch.full_like(ids, -1))
+    keep = loc >= 0
+    tw = torch.where(keep, torch.as_tensor(topk_weights).float(), torch.zeros(()))
+    return tw, torch.where(keep, loc, torch.zeros_like(loc)).to(torch.int32)
 
 
 def fused_experts_bias(x, w13, b13, w2, b2, topk_weights, topk_ids,

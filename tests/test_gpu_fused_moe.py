@@ -255,3 +255,31 @@ def test_bias_swiglu(M, alpha, limit, on_input):
                                apply_router_weight_on_input=on_input,
                                alpha=1.0 if alpha is None else alpha, limit=limit)
     _close(out, ref, 2e-2)
+
+
+# ------------------------------------------------------------ expert parallel
+@pytest.mark.parametrize("M", [3, 200])
+def test_expert_map(M):
+    """expert_map / global_num_experts (ops/fused_moe.py:145-146,160): identity
+    map equals no map bit for bit; a two-rank split matches the oracle per rank
+    and the partials sum to the single-rank output."""
+    K, N, E, k = 256, 384, 16, 4
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    x, w13, w2 = d["x"].to(DEV), d["w13"].to(DEV), d["w2"].to(DEV)
+    tw, ti = d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    full = flaggems_sglang.fused_experts(x, w13, w2, tw, ti)
+    ident = flaggems_sglang.fused_experts(x, w13, w2, tw, ti, expert_map=torch.arange(E, device=DEV),
+                                          global_num_experts=E)
+    assert torch.equal(full, ident)
+    parts = []
+    for r in range(2):
+        emap = torch.full((E,), -1, dtype=torch.int32)
+        emap[r::2] = torch.arange(E // 2, dtype=torch.int32)      # rank r owns experts r, r+2, ...
+        lw13, lw2 = d["w13"][r::2].contiguous(), d["w2"][r::2].contiguous()
+        out = flaggems_sglang.fused_experts(x, lw13.to(DEV), lw2.to(DEV), tw, ti,
+                                            expert_map=emap.to(DEV), global_num_experts=E)
+        ltw, lti = O.ep_localize(d["topk_weights"], d["topk_ids"], emap)
+        _close(out, O.fused_experts(d["x"], lw13, lw2, ltw, lti), 2e-2)
+        parts.append(out.float())
+    _close(parts[0] + parts[1], O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"],
+                                                d["topk_ids"]).float(), 2e-2)

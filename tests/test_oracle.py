@@ -405,3 +405,21 @@ def test_fused_experts_bias_zero_weights_closed_form():
     got = O.fused_experts_bias(d["x"], z13, b13, z2, b2, d["topk_weights"], d["topk_ids"])
     want = (d["topk_weights"][..., None] * b2[d["topk_ids"].long()]).sum(1)
     assert torch.allclose(got.float(), want, atol=1e-2, rtol=1e-2)
+
+
+def test_ep_localize_identity_and_rank_sum():
+    d = O.make_inputs(11, 128, 64, 8, 3, wscale=0.1)
+    full = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"])
+    tw, ti = O.ep_localize(d["topk_weights"], d["topk_ids"], torch.arange(8))
+    same = O.fused_experts(d["x"], d["w13"], d["w2"], tw, ti)
+    assert torch.equal(full, same)
+    # two ranks owning experts {0..3} and {4..7}: partial outputs sum to the
+    # full one (up to the bf16 rounding of each partial)
+    parts = []
+    for r in range(2):
+        emap = torch.full((8,), -1)
+        emap[4 * r:4 * r + 4] = torch.arange(4)
+        tw, ti = O.ep_localize(d["topk_weights"], d["topk_ids"], emap)
+        parts.append(O.fused_experts(d["x"], d["w13"][4 * r:4 * r + 4], d["w2"][4 * r:4 * r + 4], tw, ti))
+    s = parts[0].float() + parts[1].float()
+    assert torch.allclose(s, full.float(), atol=2e-2 * full.float().abs().max().item(), rtol=2e-2)
