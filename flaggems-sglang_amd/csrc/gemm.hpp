@@ -53,32 +53,40 @@ __host__ __device__ __forceinline__ int64_t gemm1_row(int act, int64_t n_act, in
   return act == kActSwiglu ? 2 * c + u : c + u * n_act;
 }
 
-// GEMM1 epilogue value for output column c of a slot: ga / ua are the fp32
-// GEMM results of its gate and up (linear) rows, gb / ub their biases, g the
-// routing weight when applied on the input (else 1).
+// GEMM1 epilogue value for output column c of a slot (ACT = the
+// activation, a template parameter so each kernel variant carries only its
+// own epilogue): ga / ua are the fp32 GEMM results of its gate and up
+// (linear) rows, gb / ub their biases, g the routing weight when applied on
+// the input (else 1).
+template <int ACT>
 __device__ __forceinline__ float gemm1_act(const GemmParams& p, float ga, float ua, float gb,
                                            float ub, float g) {
-  if (p.act == kActSwiglu) {
+  if constexpr (ACT == kActSwiglu) {
     float gv = ga + gb, lv = ua + ub;
     if (p.limit > 0.f) {
       gv = fminf(gv, p.limit);
       lv = fminf(fmaxf(lv, -p.limit), p.limit);
     }
     return gv / (1.0f + __expf(-p.alpha * gv)) * (lv + 1.0f) * g;
+  } else {
+    const float gv = round_bf16(ga * g), uv = round_bf16(ua * g);
+    if constexpr (ACT == kActGelu) return 0.5f * gv * (1.0f + erff(gv * 0.7071067811865476f)) * uv;
+    return silu_mul(gv, uv);
   }
-  const float gv = round_bf16(ga * g), uv = round_bf16(ua * g);
-  if (p.act == kActGelu) return 0.5f * gv * (1.0f + erff(gv * 0.7071067811865476f)) * uv;
-  return silu_mul(gv, uv);
 }
 
-// GEMM1 biases of output column c of expert e (0 without a bias).
+// GEMM1 biases of output column c of expert e (0 without a bias; only the
+// SWIGLU variant takes one).
+template <int ACT>
 __device__ __forceinline__ void gemm1_bias(const GemmParams& p, int e, int64_t c, float& gb,
                                            float& ub) {
   gb = ub = 0.f;
-  if (p.bias) {
-    const float* b = p.bias + static_cast<int64_t>(e) * p.Nout;
-    gb = b[gemm1_row(p.act, p.N_act, c, 0)];
-    ub = b[gemm1_row(p.act, p.N_act, c, 1)];
+  if constexpr (ACT == kActSwiglu) {
+    if (p.bias) {
+      const float* b = p.bias + static_cast<int64_t>(e) * p.Nout;
+      gb = b[gemm1_row(ACT, p.N_act, c, 0)];
+      ub = b[gemm1_row(ACT, p.N_act, c, 1)];
+    }
   }
 }
 

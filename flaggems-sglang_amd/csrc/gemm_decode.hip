@@ -78,7 +78,7 @@ constexpr int pipe_depth(WType wt, Mode mode) {
   return wt == WType::kFp8 && mode == Mode::kGemm1Silu ? 2 : 1;
 }
 
-template <WType WT, Mode MODE, int PIPE>
+template <WType WT, Mode MODE, int PIPE, int ACT>
 __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
   __shared__ f32x4_t red[kWaves][NI][kWave];
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
     int64_t r;
     if (MODE == Mode::kGemm1Silu) {
       int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + (lane & 15);
-      r = gemm1_row(p.act, p.N_act, jj, j < NI / 2 ? 0 : 1);
+      r = gemm1_row(ACT, p.N_act, jj, j < NI / 2 ? 0 : 1);
     } else {
       r = static_cast<int64_t>(nt) * BN + j * 16 + (lane & 15);
       if (r >= p.Nout) r = p.Nout - 1;
@@ -318,8 +318,8 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
       for (int j = 0; j < NI / 2; ++j) {
         const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + j * 16 + col16;
         float gb, ub;
-        gemm1_bias(p, e, col, gb, ub);
-        act[col] = f32_to_bf16(gemm1_act(p, acc[j][r], acc[j + NI / 2][r], gb, ub, g));
+        gemm1_bias<ACT>(p, e, col, gb, ub);
+        act[col] = f32_to_bf16(gemm1_act<ACT>(p, acc[j][r], acc[j + NI / 2][r], gb, ub, g));
       }
     } else {
       float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
@@ -347,21 +347,26 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   dim3 g(static_cast<unsigned>(p.max_tiles), static_cast<unsigned>(p.n_ntiles),
          static_cast<unsigned>(mode == Mode::kGemm2 ? p.splits : 1));
   dim3 b(decode::kThreads);
-#define LAUNCH(WT_, MODE_)                                                            \
-  decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_)><<<g, b, 0, s>>>(p)
+#define LAUNCH(WT_, MODE_, ACT_) \
+  decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_><<<g, b, 0, s>>>(p)
+#define LAUNCH_G1(WT_)                                                 \
+  (p.act == kActSwiglu ? LAUNCH(WT_, Mode::kGemm1Silu, kActSwiglu)     \
+   : p.act == kActGelu ? LAUNCH(WT_, Mode::kGemm1Silu, kActGelu)       \
+                       : LAUNCH(WT_, Mode::kGemm1Silu, kActSilu))
   if (mode == Mode::kGemm1Silu) {
     switch (wt) {
-      case WType::kBf16: LAUNCH(WType::kBf16, Mode::kGemm1Silu); break;
-      case WType::kFp8: LAUNCH(WType::kFp8, Mode::kGemm1Silu); break;
-      case WType::kInt4: LAUNCH(WType::kInt4, Mode::kGemm1Silu); break;
+      case WType::kBf16: LAUNCH_G1(WType::kBf16); break;
+      case WType::kFp8: LAUNCH_G1(WType::kFp8); break;
+      case WType::kInt4: LAUNCH_G1(WType::kInt4); break;
     }
   } else {
     switch (wt) {
-      case WType::kBf16: LAUNCH(WType::kBf16, Mode::kGemm2); break;
-      case WType::kFp8: LAUNCH(WType::kFp8, Mode::kGemm2); break;
-      case WType::kInt4: LAUNCH(WType::kInt4, Mode::kGemm2); break;
+      case WType::kBf16: LAUNCH(WType::kBf16, Mode::kGemm2, kActSilu); break;
+      case WType::kFp8: LAUNCH(WType::kFp8, Mode::kGemm2, kActSilu); break;
+      case WType::kInt4: LAUNCH(WType::kInt4, Mode::kGemm2, kActSilu); break;
     }
   }
+#undef LAUNCH_G1
 #undef LAUNCH
   return fmoe_host::check_launch("gemm_decode");
 }

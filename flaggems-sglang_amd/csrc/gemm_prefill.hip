@@ -159,7 +159,7 @@ __device__ __forceinline__ void quad_transpose(f32x4_t& v, int lane) {
   }
 }
 
-template <class C>
+template <class C, int ACT>
 __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, MI = C::MI, NI = C::NI;
   constexpr int SB = C::SB, UPB = C::UPB, NW = C::NW, NBUF = C::NBUF;
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       if (MODE == Mode::kGemm1Silu) {
         const int w = r / WN, within = r % WN;
         const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + w * (WN / 2) + (within % (WN / 2));
-        brow = gemm1_row(p.act, p.N_act, j, within < WN / 2 ? 0 : 1);
+        brow = gemm1_row(ACT, p.N_act, j, within < WN / 2 ? 0 : 1);
       } else {
         brow = static_cast<int64_t>(nt) * BN + r;
         if (brow >= p.Nout) brow = p.Nout - 1;
@@ -257,8 +257,8 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     if (MODE == Mode::kGemm1Silu) {
       // the wave's gate rows (and up rows) lie in one 128-row scale block
       const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2);
-      s0 = se + (gemm1_row(p.act, p.N_act, j, 0) / 128) * ksb;
-      s1 = se + (gemm1_row(p.act, p.N_act, j, 1) / 128) * ksb;
+      s0 = se + (gemm1_row(ACT, p.N_act, j, 0) / 128) * ksb;
+      s1 = se + (gemm1_row(ACT, p.N_act, j, 1) / 128) * ksb;
     } else {
       int64_t j = static_cast<int64_t>(nt) * BN + wn * WN;
       if (j >= p.Nout) j = p.Nout - 1;
@@ -388,8 +388,8 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             float gb, ub;
-            gemm1_bias(p, e, col + 2 * c + h, gb, ub);
-            a[h] = gemm1_act(p, gv[2 * c + h], uv[2 * c + h], gb, ub, g);
+            gemm1_bias<ACT>(p, e, col + 2 * c + h, gb, ub);
+            a[h] = gemm1_act<ACT>(p, gv[2 * c + h], uv[2 * c + h], gb, ub, g);
           }
           w[c] = f32_to_bf16(a[0]) | (static_cast<uint32_t>(f32_to_bf16(a[1])) << 16);
         }
@@ -429,7 +429,13 @@ int launch(const GemmParams& p0, hipStream_t s) {
   if (C::FP8 && p.Kred / 128 > kMaxKStages)
     return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill fp8: reduction dim %lld is not supported",
                            static_cast<long long>(p.Kred));
-  gemm_prefill_kernel<C><<<dim3(static_cast<unsigned>(grid)), dim3(C::NT), 0, s>>>(p);
+  const dim3 g(static_cast<unsigned>(grid)), b(C::NT);
+  if (C::MODE == Mode::kGemm2 || p.act == kActSilu)
+    gemm_prefill_kernel<C, kActSilu><<<g, b, 0, s>>>(p);
+  else if (p.act == kActGelu)
+    gemm_prefill_kernel<C, kActGelu><<<g, b, 0, s>>>(p);
+  else
+    gemm_prefill_kernel<C, kActSwiglu><<<g, b, 0, s>>>(p);
   return fmoe_host::check_launch("gemm_prefill");
 }
 
