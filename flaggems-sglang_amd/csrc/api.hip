@@ -4,6 +4,8 @@
 namespace fmoe {
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s);
 int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
+int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
+                 float scale, void* out, hipStream_t s);
 }  // namespace fmoe
 
 using namespace fmoe;
@@ -298,6 +300,61 @@ FusedLayout layout(const fmoe_fused_args* a) {
   return L;
 }
 
+// Tiny decode batches: every tile holds at most 16 slots and the whole
+// routing fits one workgroup's LDS, so the GEMM workgroups compute their own
+// tile from the top-k ids (no align launch); rows are flat slots t * k + j.
+// bf16 / fp8 only: for int4 the separate align launch measured faster (its
+// GEMMs are short enough that the in-workgroup routing latency shows).
+bool tiny_decode(const fmoe_fused_args* a, const FusedLayout& L) {
+  return L.bm == kDecodeBM && a->wtype != FMOE_W_INT4 && a->M <= 16 && a->M * a->top_k <= 512 &&
+         a->E <= 1024 && !a->expert_map;
+}
+
+int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStream_t s) {
+  const int64_t slots = a->M * a->top_k;
+  GemmParams g1{};
+  g1.top_k = a->top_k;
+  g1.n_experts = a->E;
+  g1.max_tiles = static_cast<int>(fmoe_max_tiles(slots, a->E));
+  g1.splits = 1;
+  g1.alpha = a->alpha;
+  g1.limit = a->limit;
+  g1.act = a->activation;
+  g1.tiny_ids = a->topk_ids;
+  g1.tiny_w = a->topk_weights;
+  g1.n_tokens = a->M;
+  GemmParams g2 = g1;
+  g1.A = static_cast<const uint8_t*>(a->x);
+  g1.B = static_cast<const uint8_t*>(a->w13);
+  g1.b_scale = static_cast<const float*>(a->w13_scale);
+  g1.b_gscale = static_cast<const uint16_t*>(a->w13_scale);
+  g1.b_zero = static_cast<const uint8_t*>(a->w13_zero);
+  g1.Kred = a->K;
+  g1.Nout = 2 * a->N;
+  g1.N_act = a->N;
+  g1.gamma = a->apply_router_weight_on_input;
+  g1.bias = a->b13;
+  g1.out = ws + L.act;
+  if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm1Silu, g1, s)) return st;
+  g2.act = FMOE_ACT_SILU;
+  g2.A = static_cast<const uint8_t*>(g1.out);
+  g2.B = static_cast<const uint8_t*>(a->w2);
+  g2.b_scale = static_cast<const float*>(a->w2_scale);
+  g2.b_gscale = static_cast<const uint16_t*>(a->w2_scale);
+  g2.b_zero = static_cast<const uint8_t*>(a->w2_zero);
+  g2.Kred = a->N;
+  g2.Nout = a->K;
+  g2.N_act = a->N;
+  g2.gamma = !a->apply_router_weight_on_input;
+  g2.bias = a->b2;
+  g2.out = ws + L.y;
+  g2.splits = L.splits;
+  g2.out_split_stride = slots * a->K;
+  if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm2, g2, s)) return st;
+  return moe_sum_flat(reinterpret_cast<const float*>(ws + L.y), L.splits, a->topk_ids, a->E, a->M,
+                      a->top_k, a->K, a->routed_scaling_factor, a->out, s);
+}
+
 }  // namespace
 
 extern "C" size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a) {
@@ -317,6 +374,7 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   char* ws = static_cast<char*>(a->workspace);
   auto at = [&](size_t o) { return static_cast<void*>(ws + o); };
   const int64_t slots = a->M * a->top_k;
+  if (tiny_decode(a, L)) return fused_tiny(a, L, ws, static_cast<hipStream_t>(stream));
 
   fmoe_align_out o{};
   o.expt_indx = static_cast<int32_t*>(at(L.expt_indx));

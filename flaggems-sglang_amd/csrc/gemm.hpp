@@ -39,6 +39,11 @@ struct GemmParams {
   const float* bias;
   float alpha;
   float limit;
+  // tiny-batch decode path (routing computed in each workgroup, no align
+  // launch): topk ids / weights [n_tokens * top_k]; rows are flat slots
+  const int32_t* tiny_ids;
+  const float* tiny_w;
+  int64_t n_tokens;
 };
 
 enum Act { kActSilu = 0, kActGelu = 1, kActSwiglu = 2 };

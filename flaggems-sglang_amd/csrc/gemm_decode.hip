@@ -78,26 +78,122 @@ constexpr int pipe_depth(WType wt, Mode mode) {
   return wt == WType::kFp8 && mode == Mode::kGemm1Silu ? 2 : 1;
 }
 
-template <WType WT, Mode MODE, int PIPE, int ACT>
+// Tiny batches (tiles of <= 16 slots, at most kTinySlots slots): the routing
+// of one tile computed inside the workgroup from the top-k ids, replacing
+// the align launch.  Tiles are the (expert, 16-slot block) pairs of the
+// experts in ascending order, slots of an expert in ascending flat order
+// t * k + j -- the same tiles, in the same order, as the align kernels
+// produce, so results are identical; a tile's rows are flat slot indices.
+constexpr int kTinySlots = 512;
+constexpr int kTinyExperts = 1024;
+
+struct TinyLds {
+  int cnt[kTinyExperts];
+  int ids[kTinySlots];
+  int rows[BM];
+  int info[4];     // expert, block, rows in the tile, valid
+  int scan[kWaves];
+};
+
+// Returns false when tile mt does not exist (same decision in every thread).
+__device__ bool tiny_route(const GemmParams& p, int mt, TinyLds& L) {
+  const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
+  const int E = p.n_experts;
+  const int n = static_cast<int>(p.n_tokens * p.top_k);
+  for (int e = tid; e < E; e += kThreads) L.cnt[e] = 0;
+  if (tid == 0) L.info[3] = 0;
+  __syncthreads();
+  for (int f = tid; f < n; f += kThreads) {
+    const int id = p.tiny_ids[f];
+    L.ids[f] = id;
+    if (id >= 0 && id < E) atomicAdd(&L.cnt[id], 1);
+  }
+  __syncthreads();
+  // tiles per expert = ceil(count / 16); thread t owns experts [t*per, t*per+per)
+  const int per = (E + kThreads - 1) / kThreads;
+  int mine = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < E) mine += (L.cnt[e] + BM - 1) / BM;
+  }
+  int x = mine;  // inclusive scan over the workgroup
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  if (lane == kWave - 1) L.scan[wid] = x;
+  __syncthreads();
+  int base = x - mine;
+  for (int w = 0; w < wid; ++w) base += L.scan[w];
+  if (mt >= base && mt < base + mine) {
+    int t = base;
+    for (int i = 0; i < per; ++i) {
+      const int e = tid * per + i;
+      const int nt = e < E ? (L.cnt[e] + BM - 1) / BM : 0;
+      if (mt < t + nt) {
+        const int blk = mt - t;
+        L.info[0] = e;
+        L.info[1] = blk;
+        L.info[2] = min(BM, L.cnt[e] - blk * BM);
+        L.info[3] = 1;
+        break;
+      }
+      t += nt;
+    }
+  }
+  __syncthreads();
+  if (!L.info[3]) return false;
+  // rows: the [blk*16, blk*16+16) occurrences of expert e in flat order
+  const int e = L.info[0], lo = L.info[1] * BM;
+  int run = 0;
+  for (int c0 = 0; c0 < n; c0 += kThreads) {
+    const int f = c0 + tid;
+    const bool hit = f < n && L.ids[f] == e;
+    const uint64_t m = __ballot(hit);
+    const int before = __popcll(m & ((1ull << lane) - 1ull));
+    __syncthreads();  // L.scan reuse
+    if (lane == 0) L.scan[wid] = __popcll(m);
+    __syncthreads();
+    int off = run;
+    for (int w = 0; w < wid; ++w) off += L.scan[w];
+    const int pos = off + before;
+    if (hit && pos >= lo && pos < lo + BM) L.rows[pos - lo] = f;
+    for (int w = 0; w < kWaves; ++w) run += L.scan[w];
+  }
+  __syncthreads();
+  return true;
+}
+
+template <WType WT, Mode MODE, int PIPE, int ACT, bool TINY>
 __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
   __shared__ f32x4_t red[kWaves][NI][kWave];
+  __shared__ TinyLds tiny_lds[1];  // used by the TINY variant only
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
   const int mt = blockIdx.x;
-  if (mt >= *p.n_tiles) return;
   const int nt = blockIdx.y;
   const int split = blockIdx.z;
 
-  const int tm = p.tile_map[mt];
-  const int e = tm & 0xffff, blk = tm >> 16;
-  const int row_beg = p.offs_raw[e] + blk * BM;
-  const int row_end = min(p.offs_raw[e + 1], row_beg + BM);
+  // this tile: expert e and its rows (slot of tile row r = slot_of(r), r < n_rows)
+  int e, row_beg = 0, n_rows;
+  if constexpr (TINY) {
+    if (!tiny_route(p, mt, tiny_lds[0])) return;
+    e = tiny_lds[0].info[0];
+    n_rows = tiny_lds[0].info[2];
+  } else {
+    if (mt >= *p.n_tiles) return;
+    const int tm = p.tile_map[mt];
+    e = tm & 0xffff;
+    const int blk = tm >> 16;
+    row_beg = p.offs_raw[e] + blk * BM;
+    n_rows = min(p.offs_raw[e + 1], row_beg + BM) - row_beg;
+  }
+  auto slot_of = [&](int r) { return TINY ? tiny_lds[0].rows[r] : row_beg + r; };
 
   constexpr bool kFp8 = WT == WType::kFp8;
   constexpr bool kInt4 = WT == WType::kInt4;
   // A rows: row lane%16 of the tile (bf16 for every format)
-  int s_a = row_beg + (lane & 15);
-  if (s_a >= row_end) s_a = row_beg;
-  const int64_t a_row = MODE == Mode::kGemm1Silu ? p.topk_indx[s_a] / p.top_k : s_a;
+  const int s_a = slot_of((lane & 15) < n_rows ? (lane & 15) : 0);
+  const int64_t a_row = MODE == Mode::kGemm1Silu ? (TINY ? s_a : p.topk_indx[s_a]) / p.top_k : s_a;
   const uint8_t* a_ptr = p.A + a_row * p.Kred * 2;
   // stage geometry
   constexpr int kWStage = kInt4 ? 64 : 128;          // weight bytes per row per stage
@@ -309,9 +405,10 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
   const int col16 = lane & 15;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int s = row_beg + (lane >> 4) * 4 + r;
-    if (s >= row_end) continue;
-    const float g = p.gamma ? p.gate_scal[s] : 1.0f;
+    const int rr = (lane >> 4) * 4 + r;
+    if (rr >= n_rows) continue;
+    const int s = slot_of(rr);
+    const float g = p.gamma ? (TINY ? p.tiny_w[s] : p.gate_scal[s]) : 1.0f;
     if (MODE == Mode::kGemm1Silu) {
       uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.N_act;
 #pragma unroll
@@ -347,8 +444,10 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   dim3 g(static_cast<unsigned>(p.max_tiles), static_cast<unsigned>(p.n_ntiles),
          static_cast<unsigned>(mode == Mode::kGemm2 ? p.splits : 1));
   dim3 b(decode::kThreads);
-#define LAUNCH(WT_, MODE_, ACT_) \
-  decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_><<<g, b, 0, s>>>(p)
+#define LAUNCH(WT_, MODE_, ACT_)                                                                \
+  ((p.tiny_ids && WT_ != WType::kInt4)                                                          \
+       ? decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, true><<<g, b, 0, s>>>(p) \
+       : decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, false><<<g, b, 0, s>>>(p))
 #define LAUNCH_G1(WT_)                                                 \
   (p.act == kActSwiglu ? LAUNCH(WT_, Mode::kGemm1Silu, kActSwiglu)     \
    : p.act == kActGelu ? LAUNCH(WT_, Mode::kGemm1Silu, kActGelu)       \

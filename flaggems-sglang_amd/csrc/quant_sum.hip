@@ -50,6 +50,7 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
 __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ y, int splits,
                                                       int64_t split_stride,
                                                       const int32_t* __restrict__ gate_indx,
+                                                      const int32_t* __restrict__ ids, int n_experts,
                                                       int k, int64_t K, float scale,
                                                       uint16_t* __restrict__ out) {
   const int64_t t = blockIdx.y;
@@ -57,7 +58,10 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ 
   if (c >= K) return;
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
   for (int j = 0; j < k; ++j) {
-    const int s = gate_indx[t * k + j];
+    // tiny-batch path (gate_indx null): slot = flat index, dropped when its
+    // expert id is out of range
+    const int s = gate_indx ? gate_indx[t * k + j]
+                            : (ids[t * k + j] >= 0 && ids[t * k + j] < n_experts ? static_cast<int>(t * k + j) : -1);
     if (s < 0) continue;  // slot routed to no expert
     for (int p = 0; p < splits; ++p) {
       const float4 v = *reinterpret_cast<const float4*>(y + p * split_stride + static_cast<int64_t>(s) * K + c);
@@ -107,6 +111,17 @@ extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
   dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
   moe_sum_kernel<<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
-      y, splits, M * k * K, gate_indx, k, K, scale, static_cast<uint16_t*>(out));
+      y, splits, M * k * K, gate_indx, nullptr, 0, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
+
+namespace fmoe {
+// moe_sum of the tiny-batch decode path: y rows are flat slots (t * k + j).
+int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
+                 float scale, void* out, hipStream_t s) {
+  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
+  moe_sum_kernel<<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, k, K, scale,
+                                 static_cast<uint16_t*>(out));
+  return check_launch("moe_sum");
+}
+}  // namespace fmoe

@@ -283,3 +283,28 @@ def test_expert_map(M):
         parts.append(out.float())
     _close(parts[0] + parts[1], O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"],
                                                 d["topk_ids"]).float(), 2e-2)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_tiny_decode_path_equals_aligned_path(M, fp8):
+    """fused_experts at M <= 16 (bf16 / fp8) computes each tile's routing
+    inside the GEMM workgroups instead of launching the align kernels; the
+    tiles, their row order and every sum are the same, so the output equals
+    the aligned path (triton_kernel_fused_experts) bit for bit."""
+    K, N, E, k = 512, 384, 16, 4
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    x, w13, w2 = d["x"].to(DEV), d["w13"].to(DEV), d["w2"].to(DEV)
+    tw, ti = d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    kw, tkw = {}, {}
+    if fp8:
+        w13, s13 = Q.quantize_fp8_block(w13)
+        w2, s2 = Q.quantize_fp8_block(w2)
+        kw = dict(use_fp8_w8a8=True, w1_scale=s13, w2_scale=s2, block_shape=[128, 128])
+        tkw = dict(use_fp8_w8a8=True, w1_scale=s13.transpose(1, 2), w2_scale=s2.transpose(1, 2),
+                   block_shape=[128, 128])
+    out = flaggems_sglang.fused_experts(x, w13, w2, tw, ti, **kw)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw, ti, E)
+    ref = flaggems_sglang.triton_kernel_fused_experts(x, w13.transpose(1, 2), w2.transpose(1, 2),
+                                                      rd, gi, si, **tkw)
+    assert torch.equal(out, ref)
