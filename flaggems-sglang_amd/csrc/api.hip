@@ -134,10 +134,30 @@ int check_epilogue(const fmoe_epilogue* ep, const char* who) {
 }
 }  // namespace
 
+namespace {
+int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
+               const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
+               const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep, void* act,
+               int path, int4* tile_lut, void* stream);
+int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w2,
+               const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
+               const fmoe_routing* r, int apply_gamma, const float* bias, float* y, int splits,
+               int path, int4* tile_lut, void* stream);
+}  // namespace
+
 extern "C" int fmoe_gemm1_ex(int wtype, const void* x, const float* x_scale, const void* w13,
                              const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
                              const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep,
                              void* act, int path, void* stream) {
+  return gemm1_impl(wtype, x, x_scale, w13, w13_scale, w13_zero, K, N, r, gamma_on_input, ep, act,
+                    path, nullptr, stream);
+}
+
+namespace {
+int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
+               const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
+               const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep, void* act,
+               int path, int4* tile_lut, void* stream) {
   if (int st = check_epilogue(ep, "gemm1")) return st;
   if (int st = check_routing(r, "gemm1")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm1: unknown weight type %d", wtype);
@@ -175,10 +195,12 @@ extern "C" int fmoe_gemm1_ex(int wtype, const void* x, const float* x_scale, con
     p.alpha = ep->alpha;
     p.limit = ep->limit;
   }
+  p.tile_lut = tile_lut;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (is_decode(r)) return launch_decode(to_wt(wtype), Mode::kGemm1Silu, p, s);
   return launch_prefill(to_wt(wtype), Mode::kGemm1Silu, r->block_m, p, s);
 }
+}  // namespace
 
 extern "C" int fmoe_gemm2(int wtype, const void* act, const float* act_scale, const void* w2,
                           const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
@@ -192,6 +214,15 @@ extern "C" int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale,
                              const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
                              const fmoe_routing* r, int apply_gamma, const float* bias, float* y,
                              int splits, int path, void* stream) {
+  return gemm2_impl(wtype, act, act_scale, w2, w2_scale, w2_zero, K, N, r, apply_gamma, bias, y,
+                    splits, path, nullptr, stream);
+}
+
+namespace {
+int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w2,
+               const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
+               const fmoe_routing* r, int apply_gamma, const float* bias, float* y, int splits,
+               int path, int4* tile_lut, void* stream) {
   if (int st = check_routing(r, "gemm2")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm2: unknown weight type %d", wtype);
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
@@ -227,10 +258,12 @@ extern "C" int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale,
   p.out = y;
   p.splits = splits;
   p.out_split_stride = r->n_tokens * r->top_k * K;
+  p.tile_lut = tile_lut;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (is_decode(r)) return launch_decode(to_wt(wtype), Mode::kGemm2, p, s);
   return launch_prefill(to_wt(wtype), Mode::kGemm2, r->block_m, p, s);
 }
+}  // namespace
 
 // ------------------------------------------------------------ fused path
 namespace {
@@ -240,7 +273,7 @@ struct FusedLayout {
   int splits;
   int64_t max_tiles;
   size_t align_ws, expt_indx, expt_scal, topk_indx, gate_indx, gate_scal, hist, offs_raw,
-      offs_pad, tile_map, n_tiles, xq, xs, act, actq, acts, y, total;
+      offs_pad, tile_map, n_tiles, xq, xs, act, actq, acts, y, lut, total;
 };
 
 int check_fused(const fmoe_fused_args* a) {
@@ -296,6 +329,10 @@ FusedLayout layout(const fmoe_fused_args* a) {
   L.actq = take(fp8 ? slots * a->N : 0);
   L.acts = take(fp8 ? 4 * slots * (a->N / 128) : 0);
   L.y = take(4 * static_cast<size_t>(L.splits) * slots * a->K);
+  // prefill: logical-tile table, shared by the two GEMM launches (stream order)
+  const int64_t nn1 = (a->N + kPrefillBN / 2 - 1) / (kPrefillBN / 2);
+  const int64_t nn2 = (a->K + kPrefillBN - 1) / kPrefillBN;
+  L.lut = take(L.bm == kDecodeBM ? 0 : 16 * static_cast<size_t>(L.max_tiles) * (nn1 > nn2 ? nn1 : nn2));
   L.total = off;
   return L;
 }
@@ -419,8 +456,9 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
     xs = static_cast<const float*>(at(L.xs));
   }
   fmoe_epilogue ep{a->activation, a->b13, a->alpha, a->limit};
-  if (int st = fmoe_gemm1_ex(a->wtype, x, xs, a->w13, a->w13_scale, a->w13_zero, a->K, a->N, &r,
-                             a->apply_router_weight_on_input, &ep, at(L.act), 0, stream))
+  int4* lut = L.bm == kDecodeBM ? nullptr : static_cast<int4*>(at(L.lut));
+  if (int st = gemm1_impl(a->wtype, x, xs, a->w13, a->w13_scale, a->w13_zero, a->K, a->N, &r,
+                          a->apply_router_weight_on_input, &ep, at(L.act), 0, lut, stream))
     return st;
   const void* act = at(L.act);
   const float* acts = nullptr;
@@ -431,9 +469,9 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
     act = at(L.actq);
     acts = static_cast<const float*>(at(L.acts));
   }
-  if (int st = fmoe_gemm2_ex(a->wtype, act, acts, a->w2, a->w2_scale, a->w2_zero, a->K, a->N, &r,
-                             !a->apply_router_weight_on_input, a->b2, static_cast<float*>(at(L.y)),
-                             L.splits, 0, stream))
+  if (int st = gemm2_impl(a->wtype, act, acts, a->w2, a->w2_scale, a->w2_zero, a->K, a->N, &r,
+                          !a->apply_router_weight_on_input, a->b2, static_cast<float*>(at(L.y)),
+                          L.splits, 0, lut, stream))
     return st;
   return fmoe_moe_sum(static_cast<const float*>(at(L.y)), L.splits, o.gate_indx, a->M, a->top_k,
                       a->K, a->routed_scaling_factor, a->out, stream);

@@ -34,6 +34,10 @@ struct GemmParams {
   int n_ntiles;            // output tiles along Nout
   int splits;              // GEMM2 split-K factor (decode path)
   int group_tiles;         // prefill: concurrent tiles per rasterization window (0 = default)
+  // prefill: optional [n_tiles * n_ntiles] table, logical tile ->
+  // (expert, N-tile, first row, end row), filled by a small kernel before the
+  // GEMM (replaces the dependent routing loads of every workgroup's prologue)
+  int4* tile_lut;
   // epilogue (fmoe_epilogue): activation, fp32 bias [E, Nout], swiglu alpha / limit
   int act;
   const float* bias;

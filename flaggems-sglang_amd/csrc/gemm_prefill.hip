@@ -159,6 +159,42 @@ __device__ __forceinline__ void quad_transpose(f32x4_t& v, int lane) {
   }
 }
 
+// Logical tile L (within one split) -> expert, N-tile and rows.  Per expert,
+// windows of all its T M-tiles x G N-tiles (T * G ~ group_tiles, about what
+// one XCD runs at once) are enumerated M-fastest, so the tiles that share a
+// weight panel run together on one XCD and the panel is fetched from HBM
+// once.  Called by one whole wave (find_expert ballots).
+struct Tile {
+  int e, nt, row_beg, row_end;
+};
+template <int BM>
+__device__ __forceinline__ Tile tile_of(const GemmParams& p, int L, int lane) {
+  const int nn = p.n_ntiles;
+  Tile t;
+  t.e = find_expert(p.offs_pad, p.n_experts, L, nn, lane);
+  const int t0 = p.offs_pad[t.e];
+  const int T = p.offs_pad[t.e + 1] - t0;
+  const int local = L - t0 * nn;
+  const int G = max(1, p.group_tiles / T);
+  const int grp = local / (T * G);
+  const int rr = local - grp * T * G;
+  const int blk = rr % T;
+  t.nt = grp * G + rr / T;
+  t.row_beg = p.offs_raw[t.e] + blk * BM;
+  t.row_end = min(p.offs_raw[t.e + 1], t.row_beg + BM);
+  return t;
+}
+
+// Fills p.tile_lut for every live logical tile: one wave per tile.
+template <int BM>
+__global__ __launch_bounds__(256) void tile_lut_kernel(GemmParams p) {
+  const int lane = threadIdx.x % kWave;
+  const int L = blockIdx.x * 4 + threadIdx.x / kWave;
+  if (L >= *p.n_tiles * p.n_ntiles) return;
+  const Tile t = tile_of<BM>(p, L, lane);
+  if (lane == 0) p.tile_lut[L] = int4{t.e, t.nt, t.row_beg, t.row_end};
+}
+
 template <class C, int ACT>
 __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, MI = C::MI, NI = C::NI;
@@ -173,11 +209,8 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int wm = wid / C::WAVES_N, wn = wid % C::WAVES_N;
 
-  // ---- which (split, expert M-tile, N-tile).  Workgroup ids are first made
-  // XCD-contiguous; then, per expert, windows of all its T M-tiles x G N-tiles
-  // (T * G ~ group_tiles, about what one XCD runs at once) are enumerated
-  // M-fastest, so the tiles that share a weight panel run together on one XCD
-  // and the panel is fetched from HBM once.
+  // ---- which (split, expert M-tile, N-tile): workgroup ids are made
+  // XCD-contiguous, then mapped by tile_of (or its precomputed table).
   const int nn = p.n_ntiles;
   const int per_split = *p.n_tiles * nn;
   const int live = per_split * p.splits;
@@ -185,17 +218,20 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   int L = xcd_remap(blockIdx.x, live);
   const int split = L / per_split;
   L -= split * per_split;
-  const int e = find_expert(p.offs_pad, p.n_experts, L, nn, lane);
-  const int t0 = p.offs_pad[e];
-  const int T = p.offs_pad[e + 1] - t0;
-  const int local = L - t0 * nn;
-  const int G = max(1, p.group_tiles / T);
-  const int grp = local / (T * G);
-  const int rr = local - grp * T * G;
-  const int blk = rr % T;
-  const int nt = grp * G + rr / T;
-  const int row_beg = p.offs_raw[e] + blk * BM;
-  const int row_end = min(p.offs_raw[e + 1], row_beg + BM);
+  int e, nt, row_beg, row_end;
+  if (p.tile_lut) {
+    const int4 v = p.tile_lut[L];
+    e = v.x;
+    nt = v.y;
+    row_beg = v.z;
+    row_end = v.w;
+  } else {
+    const Tile t = tile_of<BM>(p, L, lane);
+    e = t.e;
+    nt = t.nt;
+    row_beg = t.row_beg;
+    row_end = t.row_end;
+  }
 
   const int64_t kbytes = FP8 ? p.Kred : p.Kred * 2;  // bytes per operand row
   const int nk_all = static_cast<int>(kbytes / SB);
@@ -429,6 +465,10 @@ int launch(const GemmParams& p0, hipStream_t s) {
   if (C::FP8 && p.Kred / 128 > kMaxKStages)
     return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill fp8: reduction dim %lld is not supported",
                            static_cast<long long>(p.Kred));
+  if (p.tile_lut) {
+    const int64_t lut_n = static_cast<int64_t>(p.max_tiles) * p.n_ntiles;
+    tile_lut_kernel<C::BM><<<dim3(static_cast<unsigned>((lut_n + 3) / 4)), dim3(256), 0, s>>>(p);
+  }
   const dim3 g(static_cast<unsigned>(grid)), b(C::NT);
   if (C::MODE == Mode::kGemm2 || p.act == kActSilu)
     gemm_prefill_kernel<C, kActSilu><<<g, b, 0, s>>>(p);
