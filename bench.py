@@ -362,6 +362,43 @@ def secondary_entry(res):
     return e
 
 
+def measure_repack(reps=10):
+    """Load-time int4 checkpoint repack (AWQ and GPTQ v2) of the Mixtral w13
+    shape [8, 2*14336 rows, K=4096], group 128: HBM bytes read + written per
+    call over the call's time."""
+    import torch
+
+    from flaggems_sglang import formats as F
+
+    E, K, N, g = 8, 4096, 2 * 14336, 128
+    dev = "cuda"
+    gen = torch.Generator(device=dev).manual_seed(5)
+    out = {}
+    for fmt in ("awq", "gptq_v2"):
+        shape = (E, K, N // 8) if fmt == "awq" else (E, K // 8, N)
+        qw = torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev, generator=gen)
+        qz = torch.randint(-2**31, 2**31 - 1, (E, K // g, N // 8), dtype=torch.int32, device=dev, generator=gen)
+        sc = torch.rand(E, K // g, N, device=dev, generator=gen).to(torch.float16)
+        fn = (lambda: F.repack_awq_moe(qw, qz, sc)) if fmt == "awq" else \
+            (lambda: F.repack_gptq_moe(qw, qz, sc, checkpoint_format="gptq_v2"))
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / reps / 1e3
+        nbytes = 2 * (qw.numel() * 4 + qz.numel() * 4 + sc.numel() * 2)
+        out[fmt] = {"ms": round(t * 1e3, 4), "GB/s": round(nbytes / t / 1e9, 1),
+                    "frac_hbm_peak": round(nbytes / t / 1e9 / PEAK["hbm_gbs"], 4),
+                    "bytes": nbytes}
+        del qw, qz, sc
+        torch.cuda.empty_cache()
+    return {"workload": "int4 checkpoint repack, Mixtral w13 [8, 28672, 4096], group 128", **out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -418,6 +455,7 @@ def main():
         del r
         torch.cuda.empty_cache()
     line["secondary"] = sec
+    line["repack"] = measure_repack()
     line["cpu_baseline"] = None if args.no_cpu else cpu_baseline(p)
     if args.copy_calib:
         src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)

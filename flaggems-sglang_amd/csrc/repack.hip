@@ -1,0 +1,186 @@
+// Load-time conversion of int4 MoE checkpoints (AWQ, GPTQ) into the layout the
+// W4A16 kernels read.  Integer / byte work, HBM-bound, run once per weight.
+//
+// Source formats (per expert, stacked on a leading expert dim; K = reduction
+// dim / input features, N = output rows / features, g = group size):
+//   AWQ  (AutoAWQ "gemm" packing): qweight int32 [K, N/8]: word j of row k
+//        holds columns 8j..8j+7, nibble i (bits 4i..4i+3) = column
+//        8j + kAwqOrder[i]; qzeros int32 [K/g, N/8] packed the same way;
+//        scales fp16 [K/g, N]; w = (q - z) * s.
+//   GPTQ (AutoGPTQ packing, no act-order): qweight int32 [K/8, N]: word i of
+//        column n holds rows 8i..8i+7, nibble j = row 8i + j; qzeros int32
+//        [K/g, N/8], nibble j of word c = column 8c + j; scales fp16
+//        [K/g, N].  Format v1 stores zero - 1 (w = (q - (z + 1)) * s), v2
+//        stores the zero itself.
+// Target (the W4A16 kernels): q u8 [N, K/2] (row n, reduction element 2i in
+// the low nibble, 2i+1 in the high), scales fp16 [K/g, N] (unchanged), zeros
+// u8 [K/g, N/2] (row 2j low nibble, 2j+1 high).
+//
+// GPTQ words are already packed along K in the target's nibble order, so their
+// conversion is a transpose of 32-bit words; AWQ needs a 4-bit transpose,
+// staged through LDS one 128 x 128 tile at a time.
+#include "common.hpp"
+
+namespace fmoe {
+namespace repack {
+
+constexpr int kTile = 64;    // GPTQ word-transpose tile
+constexpr int kAwqTK = 128;  // AWQ nibble tile: reduction elements x output rows
+constexpr int kAwqTN = 128;  // (measured best of 64/128/256 combinations)
+constexpr int kThreads = 256;
+// column held by nibble i of an AWQ word (within its 8 columns)
+__constant__ int kAwqOrder[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+// nibble holding column c of an AWQ word (inverse of kAwqOrder)
+__constant__ int kAwqNibble[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+
+// AWQ qweight [E][K][N/8] -> q [E][N][K/2], one TK x TN tile (reduction x
+// output rows) per workgroup through an LDS nibble tile.  Grid (N/TN, K/TK, E).
+template <int TK, int TN>
+__global__ __launch_bounds__(kThreads) void awq_weight_kernel(const int32_t* __restrict__ qw,
+                                                              int64_t K, int64_t N,
+                                                              uint8_t* __restrict__ out) {
+  __shared__ uint8_t t[TN][TK + 4];  // [n][k]
+  constexpr int WPR = TN / 8;         // words per tile row
+  const int tid = threadIdx.x;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * TN;
+  const int64_t k0 = static_cast<int64_t>(blockIdx.y) * TK;
+  const int64_t e = blockIdx.z;
+  const int64_t nw = N / 8;
+  const int32_t* src = qw + e * K * nw;
+  // consecutive threads read consecutive words of a row (TN / 2 bytes)
+  for (int w = tid; w < TK * WPR; w += kThreads) {
+    const int kl = w / WPR, jl = w % WPR;
+    const int64_t k = k0 + kl, j = n0 / 8 + jl;
+    uint32_t word = 0;
+    if (k < K && j < nw) word = static_cast<uint32_t>(src[k * nw + j]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) t[8 * jl + kAwqOrder[i]][kl] = static_cast<uint8_t>((word >> (4 * i)) & 15u);
+  }
+  __syncthreads();
+  // each thread writes 8 bytes (16 reduction elements) of one output row;
+  // consecutive threads cover one row's TK / 2 bytes
+  constexpr int PPR = TK / 16;  // 8-byte pieces per row
+  for (int w = tid; w < TN * PPR; w += kThreads) {
+    const int nl = w / PPR, part = w % PPR;
+    const int64_t n = n0 + nl;
+    if (n >= N) continue;
+    uint8_t* dst = out + (e * N + n) * (K / 2);
+    uint32_t b[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int kl = 16 * part + 2 * i;
+      const uint32_t byte = t[nl][kl] | (t[nl][kl + 1] << 4);
+      b[i / 4] |= byte << (8 * (i % 4));
+    }
+    const int64_t kb = k0 + 16 * part;  // first reduction element of these 8 bytes
+    if (kb + 16 <= K) {
+      *reinterpret_cast<uint2*>(dst + kb / 2) = make_uint2(b[0], b[1]);
+    } else {
+      for (int i = 0; i < 8 && kb + 2 * i < K; ++i) dst[kb / 2 + i] = static_cast<uint8_t>(b[i / 4] >> (8 * (i % 4)));
+    }
+  }
+}
+
+// GPTQ qweight [E][K/8][N] -> q [E][N][K/2] viewed as words [E][N][K/8]: a
+// 32-bit transpose.  Grid (N/64, K8/64, E), 256 threads.
+__global__ __launch_bounds__(kThreads) void gptq_weight_kernel(const uint32_t* __restrict__ qw,
+                                                               int64_t K8, int64_t N,
+                                                               uint32_t* __restrict__ out) {
+  __shared__ uint32_t t[kTile][kTile + 1];  // [i][n]
+  const int tid = threadIdx.x;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTile;
+  const int64_t i0 = static_cast<int64_t>(blockIdx.y) * kTile;
+  const int64_t e = blockIdx.z;
+  const uint32_t* src = qw + e * K8 * N;
+  for (int w = tid; w < kTile * kTile; w += kThreads) {
+    const int il = w / kTile, nl = w % kTile;  // consecutive threads: consecutive n
+    const int64_t i = i0 + il, n = n0 + nl;
+    t[il][nl] = (i < K8 && n < N) ? src[i * N + n] : 0u;
+  }
+  __syncthreads();
+  uint32_t* dst = out + e * N * K8;
+  for (int w = tid; w < kTile * kTile; w += kThreads) {
+    const int nl = w / kTile, il = w % kTile;  // consecutive threads: consecutive i
+    const int64_t i = i0 + il, n = n0 + nl;
+    if (i < K8 && n < N) dst[n * K8 + i] = t[il][nl];
+  }
+}
+
+// Zeros and scales: one thread per output zero byte (rows 2p, 2p+1 of group
+// g of expert e).  `bad` counts GPTQ v1 zeros that overflow 4 bits.
+__global__ __launch_bounds__(kThreads) void zeros_scales_kernel(int fmt, const uint32_t* __restrict__ qz,
+                                                                const uint16_t* __restrict__ sc,
+                                                                int64_t total_pairs, int64_t N,
+                                                                uint8_t* __restrict__ zo,
+                                                                uint16_t* __restrict__ so,
+                                                                int32_t* __restrict__ bad) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= total_pairs) return;
+  const int64_t half = N / 2;
+  const int64_t row = idx / half;  // (e, g) flattened
+  const int64_t p = idx % half;
+  uint32_t z[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t c = 2 * p + h;
+    const uint32_t word = qz[row * (N / 8) + c / 8];
+    const int nib = fmt == FMOE_INT4_AWQ ? kAwqNibble[c % 8] : static_cast<int>(c % 8);
+    uint32_t v = (word >> (4 * nib)) & 15u;
+    if (fmt == FMOE_INT4_GPTQ_V1) {
+      v += 1u;
+      if (v > 15u && bad) atomicAdd(bad, 1);
+      v &= 15u;
+    }
+    z[h] = v;
+  }
+  zo[idx] = static_cast<uint8_t>(z[0] | (z[1] << 4));
+  so[row * N + 2 * p] = sc[row * N + 2 * p];
+  so[row * N + 2 * p + 1] = sc[row * N + 2 * p + 1];
+}
+
+}  // namespace repack
+}  // namespace fmoe
+
+extern "C" int fmoe_repack_int4(int format, const int32_t* qweight, const int32_t* qzeros,
+                                const uint16_t* scales, int64_t E, int64_t K, int64_t N,
+                                int group, uint8_t* q_out, uint16_t* scales_out,
+                                uint8_t* zeros_out, int32_t* bad_zeros, void* stream) {
+  using namespace fmoe::repack;
+  if (format != FMOE_INT4_AWQ && format != FMOE_INT4_GPTQ_V1 && format != FMOE_INT4_GPTQ_V2)
+    return fmoe_host::fail(FMOE_ERR_INVALID, "repack_int4: unknown format %d", format);
+  if (!qweight || !qzeros || !scales || !q_out || !scales_out || !zeros_out)
+    return fmoe_host::fail(FMOE_ERR_INVALID, "repack_int4: null pointer");
+  if (E < 1 || K < 1 || N < 1 || group < 8)
+    return fmoe_host::fail(FMOE_ERR_INVALID, "repack_int4: bad sizes E=%lld K=%lld N=%lld group=%d",
+                           static_cast<long long>(E), static_cast<long long>(K),
+                           static_cast<long long>(N), group);
+  if (N % 8 || K % 8 || group % 8 || K % group)
+    return fmoe_host::fail(FMOE_ERR_INVALID,
+                           "repack_int4: need N %% 8 == 0, K %% group == 0 and group %% 8 == 0 "
+                           "(K=%lld N=%lld group=%d)",
+                           static_cast<long long>(K), static_cast<long long>(N), group);
+  if (E > 65535 || (N + kTile - 1) / kTile > 0x7fffffff || (K + kTile - 1) / kTile > 65535)
+    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "repack_int4: tensor too large for one launch");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned gx = static_cast<unsigned>((N + kTile - 1) / kTile);
+  if (format == FMOE_INT4_AWQ) {
+    constexpr int TK = kAwqTK, TN = kAwqTN;
+    const dim3 g(static_cast<unsigned>((N + TN - 1) / TN), static_cast<unsigned>((K + TK - 1) / TK),
+                 static_cast<unsigned>(E));
+    awq_weight_kernel<TK, TN><<<g, kThreads, 0, s>>>(qweight, K, N, q_out);
+  } else {
+    const int64_t K8 = K / 8;
+    const dim3 g(gx, static_cast<unsigned>((K8 + kTile - 1) / kTile), static_cast<unsigned>(E));
+    gptq_weight_kernel<<<g, kThreads, 0, s>>>(reinterpret_cast<const uint32_t*>(qweight), K8, N,
+                                              reinterpret_cast<uint32_t*>(q_out));
+  }
+  int st = fmoe_host::check_launch("repack_int4 weights");
+  if (st != FMOE_OK) return st;
+  const int64_t pairs = E * (K / group) * (N / 2);
+  const int64_t blocks = (pairs + kThreads - 1) / kThreads;
+  if (blocks > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "repack_int4: too many groups");
+  zeros_scales_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, s>>>(
+      format, reinterpret_cast<const uint32_t*>(qzeros), scales, pairs, N, zeros_out, scales_out,
+      bad_zeros);
+  return fmoe_host::check_launch("repack_int4 zeros");
+}

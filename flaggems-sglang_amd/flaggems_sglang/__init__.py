@@ -17,7 +17,7 @@ from flaggems_sglang.ops.fused_moe import (  # noqa: F401
     triton_kernel_fused_experts,
     triton_kernel_fused_experts_with_bias,
 )
-from flaggems_sglang import quant  # noqa: F401
+from flaggems_sglang import formats, quant  # noqa: F401
 
 device = "cuda"  # torch's device string for HIP devices on ROCm
 vendor_name = "amd"

@@ -588,7 +588,10 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
     ``obj.runner.config`` (``num_experts``, ``no_combine``, ``activation``,
     ``apply_router_weight_on_input``, ``routed_scaling_factor``).
     fp8 block-scale layers carry ``w13_weight_scale_inv``/``w2_weight_scale_inv``;
-    int4 layers ``w13_qweight``/``w13_scales``/``w13_qzeros`` and the w2 ones.
+    int4 layers ``w13_qweight``/``w13_scales``/``w13_qzeros`` and the w2 ones,
+    in the W4A16 layout -- or in a checkpoint layout named by
+    ``layer.fmoe_int4_checkpoint_format`` ("awq", "gptq", "gptq_v2"), which the
+    first call converts in place (``formats.repack_layer_int4``).
     """
     cfg = obj.runner.config
     b13 = getattr(layer, "w13_weight_bias", None)
@@ -602,6 +605,11 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
     on_input = bool(getattr(cfg, "apply_router_weight_on_input", False))
 
     if hasattr(layer, "w13_qweight"):
+        ckpt_format = getattr(layer, "fmoe_int4_checkpoint_format", None)
+        if ckpt_format is not None:
+            from flaggems_sglang.formats import repack_layer_int4
+
+            repack_layer_int4(layer, ckpt_format)
         quant = dict(use_int4_w4a16=True, w1_scale=layer.w13_scales, w2_scale=layer.w2_scales,
                      w1_zp=layer.w13_qzeros, w2_zp=layer.w2_qzeros)
         w13, w2 = layer.w13_qweight, layer.w2_qweight

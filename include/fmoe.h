@@ -288,6 +288,36 @@ typedef struct fmoe_fused_args {
 size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a);
 int fmoe_fused_experts(const fmoe_fused_args* a, void* stream);
 
+/* ------------------------------------------------ checkpoint weight formats
+ * Load-time repack of int4 MoE checkpoints into the FMOE_W_INT4 layout, once
+ * per weight instead of per call (the reference re-lays weights out on every
+ * forward, ops/fused_moe.py:326-327, and has no int4 path; the formats are
+ * those SGLang loads for W4A16 MoE layers).  Per expert (stacked on a leading
+ * E dim), K = reduction dim, N = output rows, g = group:
+ *   FMOE_INT4_AWQ     qweight int32 [E, K, N/8], 8 columns per word in AutoAWQ
+ *                     order (nibble i = column 8j + {0,2,4,6,1,3,5,7}[i]);
+ *                     qzeros int32 [E, K/g, N/8] same packing; w = (q - z) * s
+ *   FMOE_INT4_GPTQ_V1 qweight int32 [E, K/8, N] (nibble j of word i = row
+ *                     8i + j); qzeros int32 [E, K/g, N/8] (nibble j = column
+ *                     8c + j) holding zero - 1; no act-order (group of row k is
+ *                     k / g)
+ *   FMOE_INT4_GPTQ_V2 as V1 with the zero itself stored
+ *   scales            fp16 [E, K/g, N] for all three
+ * Outputs: q_out u8 [E, N, K/2], scales_out fp16 [E, K/g, N], zeros_out u8
+ * [E, K/g, N/2] (the fmoe_gemm1 / fmoe_fused_experts int4 layout).
+ * bad_zeros (device int32, optional, caller-zeroed) counts V1 zeros of 16,
+ * which 4 bits cannot hold (they are stored as 0).  Needs N % 8 == 0,
+ * g % 8 == 0 and K % g == 0. */
+enum fmoe_int4_format {
+  FMOE_INT4_AWQ = 0,
+  FMOE_INT4_GPTQ_V1 = 1,
+  FMOE_INT4_GPTQ_V2 = 2,
+};
+int fmoe_repack_int4(int format, const int32_t* qweight, const int32_t* qzeros,
+                     const uint16_t* scales, int64_t E, int64_t K, int64_t N, int group,
+                     uint8_t* q_out, uint16_t* scales_out, uint8_t* zeros_out,
+                     int32_t* bad_zeros, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
