@@ -6,6 +6,8 @@ int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t
 int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s);
+int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
+                 float scale, void* out, hipStream_t s);
 }  // namespace fmoe
 
 using namespace fmoe;
@@ -141,8 +143,8 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
                int path, int4* tile_lut, void* stream);
 int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w2,
                const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
-               const fmoe_routing* r, int apply_gamma, const float* bias, float* y, int splits,
-               int path, int4* tile_lut, void* stream);
+               const fmoe_routing* r, int apply_gamma, const float* bias, void* y, int splits,
+               int path, int4* tile_lut, bool y_bf16, void* stream);
 }  // namespace
 
 extern "C" int fmoe_gemm1_ex(int wtype, const void* x, const float* x_scale, const void* w13,
@@ -215,14 +217,14 @@ extern "C" int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale,
                              const fmoe_routing* r, int apply_gamma, const float* bias, float* y,
                              int splits, int path, void* stream) {
   return gemm2_impl(wtype, act, act_scale, w2, w2_scale, w2_zero, K, N, r, apply_gamma, bias, y,
-                    splits, path, nullptr, stream);
+                    splits, path, nullptr, false, stream);
 }
 
 namespace {
 int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w2,
                const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
-               const fmoe_routing* r, int apply_gamma, const float* bias, float* y, int splits,
-               int path, int4* tile_lut, void* stream) {
+               const fmoe_routing* r, int apply_gamma, const float* bias, void* y, int splits,
+               int path, int4* tile_lut, bool y_bf16, void* stream) {
   if (int st = check_routing(r, "gemm2")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm2: unknown weight type %d", wtype);
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
@@ -256,6 +258,7 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
   p.gamma = apply_gamma;
   p.bias = bias;
   p.out = y;
+  p.y_bf16 = y_bf16 && !is_decode(r) && splits == 1;
   p.splits = splits;
   p.out_split_stride = r->n_tokens * r->top_k * K;
   p.tile_lut = tile_lut;
@@ -271,6 +274,7 @@ namespace {
 struct FusedLayout {
   int bm;
   int splits;
+  bool y_bf16;
   int64_t max_tiles;
   size_t align_ws, expt_indx, expt_scal, topk_indx, gate_indx, gate_scal, hist, offs_raw,
       offs_pad, tile_map, n_tiles, xq, xs, act, actq, acts, y, lut, total;
@@ -328,7 +332,9 @@ FusedLayout layout(const fmoe_fused_args* a) {
   L.act = take(2 * slots * a->N);
   L.actq = take(fp8 ? slots * a->N : 0);
   L.acts = take(fp8 ? 4 * slots * (a->N / 128) : 0);
-  L.y = take(4 * static_cast<size_t>(L.splits) * slots * a->K);
+  // prefill with one split: bf16 rows (see fused path); otherwise fp32 planes
+  L.y_bf16 = L.bm != kDecodeBM && L.splits == 1;
+  L.y = take((L.y_bf16 ? 2 : 4) * static_cast<size_t>(L.splits) * slots * a->K);
   // prefill: logical-tile table, shared by the two GEMM launches (stream order)
   const int64_t nn1 = (a->N + kPrefillBN / 2 - 1) / (kPrefillBN / 2);
   const int64_t nn2 = (a->K + kPrefillBN - 1) / kPrefillBN;
@@ -469,10 +475,16 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
     act = at(L.actq);
     acts = static_cast<const float*>(at(L.acts));
   }
+  // Prefill without split-K keeps each slot's GEMM2 row in bf16 until the
+  // top-k sum (SGLang's per-slot intermediate has the same rounding point);
+  // split-K planes and the decode path stay fp32.
   if (int st = gemm2_impl(a->wtype, act, acts, a->w2, a->w2_scale, a->w2_zero, a->K, a->N, &r,
-                          !a->apply_router_weight_on_input, a->b2, static_cast<float*>(at(L.y)),
-                          L.splits, 0, lut, stream))
+                          !a->apply_router_weight_on_input, a->b2, at(L.y), L.splits, 0, lut,
+                          L.y_bf16, stream))
     return st;
+  if (L.y_bf16)
+    return moe_sum_bf16(static_cast<const uint16_t*>(at(L.y)), o.gate_indx, a->M, a->top_k, a->K,
+                        a->routed_scaling_factor, a->out, static_cast<hipStream_t>(stream));
   return fmoe_moe_sum(static_cast<const float*>(at(L.y)), L.splits, o.gate_indx, a->M, a->top_k,
                       a->K, a->routed_scaling_factor, a->out, stream);
 }

@@ -30,6 +30,7 @@ struct GemmParams {
   int max_tiles;
   int gamma;               // multiply rows by gate_scal[slot]
   void* out;               // GEMM1: act bf16 [M*k, N]; GEMM2: y fp32 [splits][M*k, Nout]
+  int y_bf16;              // prefill GEMM2 with one split: y rows stored as bf16 instead
   int64_t out_split_stride;  // elements between split partials (GEMM2)
   int n_ntiles;            // output tiles along Nout
   int splits;              // GEMM2 split-K factor (decode path)

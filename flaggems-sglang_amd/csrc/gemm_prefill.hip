@@ -444,8 +444,18 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) v[c] += b[c];
         }
-        if (ok && col < p.Nout)
-          *reinterpret_cast<float4*>(y + col) = make_float4(v[0] * g, v[1] * g, v[2] * g, v[3] * g);
+        if (ok && col < p.Nout) {
+          if (p.y_bf16) {
+            // one split: the row goes out as bf16, like SGLang's per-slot
+            // intermediate before its top-k sum
+            uint16_t* yb = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.Nout + col;
+            const uint32_t w0 = f32_to_bf16(v[0] * g) | (static_cast<uint32_t>(f32_to_bf16(v[1] * g)) << 16);
+            const uint32_t w1 = f32_to_bf16(v[2] * g) | (static_cast<uint32_t>(f32_to_bf16(v[3] * g)) << 16);
+            *reinterpret_cast<uint2*>(yb) = make_uint2(w0, w1);
+          } else {
+            *reinterpret_cast<float4*>(y + col) = make_float4(v[0] * g, v[1] * g, v[2] * g, v[3] * g);
+          }
+        }
       }
     }
   }

@@ -47,7 +47,8 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
 
 // out[t, c] = bf16(scale * sum_j sum_p y[p][gate_indx[t*k+j], c]); j then p
 // in ascending order.  One thread = 4 columns (16-byte loads).
-__global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ y, int splits,
+template <typename YT>
+__global__ __launch_bounds__(256) void moe_sum_kernel(const YT* __restrict__ y, int splits,
                                                       int64_t split_stride,
                                                       const int32_t* __restrict__ gate_indx,
                                                       const int32_t* __restrict__ ids, int n_experts,
@@ -64,11 +65,20 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const float* __restrict__ 
                             : (ids[t * k + j] >= 0 && ids[t * k + j] < n_experts ? static_cast<int>(t * k + j) : -1);
     if (s < 0) continue;  // slot routed to no expert
     for (int p = 0; p < splits; ++p) {
-      const float4 v = *reinterpret_cast<const float4*>(y + p * split_stride + static_cast<int64_t>(s) * K + c);
-      a0 += v.x;
-      a1 += v.y;
-      a2 += v.z;
-      a3 += v.w;
+      const YT* src = y + p * split_stride + static_cast<int64_t>(s) * K + c;
+      if constexpr (sizeof(YT) == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(src);
+        a0 += v.x;
+        a1 += v.y;
+        a2 += v.z;
+        a3 += v.w;
+      } else {  // bf16 rows
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        a0 += __uint_as_float(v.x << 16);
+        a1 += __uint_as_float(v.x & 0xffff0000u);
+        a2 += __uint_as_float(v.y << 16);
+        a3 += __uint_as_float(v.y & 0xffff0000u);
+      }
     }
   }
   const uint32_t w0 = f32_to_bf16(a0 * scale) | (static_cast<uint32_t>(f32_to_bf16(a1 * scale)) << 16);
@@ -110,7 +120,7 @@ extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx
                              static_cast<long long>(M));
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
   dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
-  moe_sum_kernel<<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
+  moe_sum_kernel<float><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
       y, splits, M * k * K, gate_indx, nullptr, 0, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
@@ -120,8 +130,16 @@ namespace fmoe {
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
   dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
-  moe_sum_kernel<<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, k, K, scale,
-                                 static_cast<uint16_t*>(out));
+  moe_sum_kernel<float><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, k, K, scale,
+                                        static_cast<uint16_t*>(out));
+  return check_launch("moe_sum");
+}
+// moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
+int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
+                 float scale, void* out, hipStream_t s) {
+  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
+  moe_sum_kernel<__bf16><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
+                                         nullptr, 0, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 }  // namespace fmoe
