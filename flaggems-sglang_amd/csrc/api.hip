@@ -140,7 +140,7 @@ namespace {
 int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
                const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
                const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep, void* act,
-               int path, int4* tile_lut, void* stream);
+               int path, int4* tile_lut, uint8_t* act_q, float* act_qs, void* stream);
 int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w2,
                const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
                const fmoe_routing* r, int apply_gamma, const float* bias, void* y, int splits,
@@ -152,21 +152,21 @@ extern "C" int fmoe_gemm1_ex(int wtype, const void* x, const float* x_scale, con
                              const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep,
                              void* act, int path, void* stream) {
   return gemm1_impl(wtype, x, x_scale, w13, w13_scale, w13_zero, K, N, r, gamma_on_input, ep, act,
-                    path, nullptr, stream);
+                    path, nullptr, nullptr, nullptr, stream);
 }
 
 namespace {
 int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
                const void* w13_scale, const void* w13_zero, int64_t K, int64_t N,
                const fmoe_routing* r, int gamma_on_input, const fmoe_epilogue* ep, void* act,
-               int path, int4* tile_lut, void* stream) {
+               int path, int4* tile_lut, uint8_t* act_q, float* act_qs, void* stream) {
   if (int st = check_epilogue(ep, "gemm1")) return st;
   if (int st = check_routing(r, "gemm1")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm1: unknown weight type %d", wtype);
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
     return fail(FMOE_ERR_UNSUPPORTED, "gemm1: K=%lld N=%lld must be multiples of 128",
                 static_cast<long long>(K), static_cast<long long>(N));
-  if (!x || !w13 || !act) return fail(FMOE_ERR_INVALID, "gemm1: null pointer");
+  if (!x || !w13 || (!act && !act_q)) return fail(FMOE_ERR_INVALID, "gemm1: null pointer");
   if (wtype == FMOE_W_FP8 && !w13_scale)
     return fail(FMOE_ERR_INVALID, "gemm1: fp8 needs w13_scale");
   if (wtype == FMOE_W_FP8 && !is_decode(r) && !x_scale)
@@ -198,6 +198,8 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
     p.limit = ep->limit;
   }
   p.tile_lut = tile_lut;
+  p.act_q = act_q;  // only the fp8 prefill kernels take it (the fused path checks)
+  p.act_qs = act_qs;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (is_decode(r)) return launch_decode(to_wt(wtype), Mode::kGemm1Silu, p, s);
   return launch_prefill(to_wt(wtype), Mode::kGemm1Silu, r->block_m, p, s);
@@ -329,7 +331,7 @@ FusedLayout layout(const fmoe_fused_args* a) {
   const bool fp8 = a->wtype == FMOE_W_FP8 && L.bm != kDecodeBM;
   L.xq = take(fp8 ? a->M * a->K : 0);
   L.xs = take(fp8 ? 4 * a->M * (a->K / 128) : 0);
-  L.act = take(2 * slots * a->N);
+  L.act = take(fp8 ? 0 : 2 * slots * a->N);  // fp8 prefill: GEMM1 writes the quantized act
   L.actq = take(fp8 ? slots * a->N : 0);
   L.acts = take(fp8 ? 4 * slots * (a->N / 128) : 0);
   // prefill with one split: bf16 rows (see fused path); otherwise fp32 planes
@@ -463,18 +465,16 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   }
   fmoe_epilogue ep{a->activation, a->b13, a->alpha, a->limit};
   int4* lut = L.bm == kDecodeBM ? nullptr : static_cast<int4*>(at(L.lut));
+  // fp8 prefill: the GEMM1 epilogue quantizes the activation (1x128 groups,
+  // bit-identical to fmoe_quant_fp8_group on its bf16 rows)
+  uint8_t* actq = fp8 ? static_cast<uint8_t*>(at(L.actq)) : nullptr;
+  float* actqs = fp8 ? static_cast<float*>(at(L.acts)) : nullptr;
   if (int st = gemm1_impl(a->wtype, x, xs, a->w13, a->w13_scale, a->w13_zero, a->K, a->N, &r,
-                          a->apply_router_weight_on_input, &ep, at(L.act), 0, lut, stream))
+                          a->apply_router_weight_on_input, &ep, fp8 ? nullptr : at(L.act), 0, lut,
+                          actq, actqs, stream))
     return st;
-  const void* act = at(L.act);
-  const float* acts = nullptr;
-  if (fp8) {
-    if (int st = fmoe_quant_fp8_group(at(L.act), slots, a->N, 128, at(L.actq),
-                                      static_cast<float*>(at(L.acts)), stream))
-      return st;
-    act = at(L.actq);
-    acts = static_cast<const float*>(at(L.acts));
-  }
+  const void* act = fp8 ? static_cast<const void*>(actq) : at(L.act);
+  const float* acts = actqs;
   // Prefill without split-K keeps each slot's GEMM2 row in bf16 until the
   // top-k sum (SGLang's per-slot intermediate has the same rounding point);
   // split-K planes and the decode path stay fp32.

@@ -31,6 +31,10 @@ struct GemmParams {
   int gamma;               // multiply rows by gate_scal[slot]
   void* out;               // GEMM1: act bf16 [M*k, N]; GEMM2: y fp32 [splits][M*k, Nout]
   int y_bf16;              // prefill GEMM2 with one split: y rows stored as bf16 instead
+  // fp8 prefill GEMM1: when set, the activation leaves the epilogue already
+  // quantized (e4m3 [M*k, N] + fp32 scales [M*k, N/128]) instead of as bf16
+  uint8_t* act_q;
+  float* act_qs;
   int64_t out_split_stride;  // elements between split partials (GEMM2)
   int n_ntiles;            // output tiles along Nout
   int splits;              // GEMM2 split-K factor (decode path)

@@ -404,6 +404,66 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   // scattered ones.
   const int orow = (lane >> 4) * 4 + (lane & 3);   // row within the 16x16 block
   const int ocol = ((lane >> 2) & 3) * 4;          // first of the lane's 4 columns
+  if constexpr (FP8 && MODE == Mode::kGemm1Silu && BN / 2 == 128) {
+    if (p.act_q) {
+      // Activation quantized here, exactly as fmoe_quant_fp8_group would do
+      // it on the bf16 activation: the tile's 128 activation columns are one
+      // 1x128 group of each row.  Row amax: the lane's 8 values, the 4 lanes
+      // holding the row's other columns of this wave, then the WAVES_N waves
+      // through LDS (the operand ring is free once every wave has left the
+      // main loop).
+      __syncthreads();
+      float* amax_lds = reinterpret_cast<float*>(&lds[0][0]);  // [BM][WAVES_N]
+      float v[MI][NI / 2][4];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int s = row_beg + wm * WM + i * 16 + orow;
+        const float g = (p.gamma && s < row_end) ? p.gate_scal[s] : 1.0f;
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < NI / 2; ++j) {
+          f32x4_t gv = acc[i][j], uv = acc[i][j + NI / 2];
+          quad_transpose(gv, lane);
+          quad_transpose(uv, lane);
+          const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2) + j * 16 + ocol;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float gb, ub;
+            gemm1_bias<ACT>(p, e, col + c, gb, ub);
+            v[i][j][c] = round_bf16(gemm1_act<ACT>(p, gv[c], uv[c], gb, ub, g));
+            amax = fmaxf(amax, fabsf(v[i][j][c]));
+          }
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 4, kWave));
+        amax = fmaxf(amax, __shfl_xor(amax, 8, kWave));
+        if (((lane >> 2) & 3) == 0) amax_lds[(wm * WM + i * 16 + orow) * C::WAVES_N + wn] = amax;
+      }
+      __syncthreads();
+      const int64_t ngrp = p.N_act / 128;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = wm * WM + i * 16 + orow;
+        const int s = row_beg + r;
+        float amax = 0.f;
+#pragma unroll
+        for (int w = 0; w < C::WAVES_N; ++w) amax = fmaxf(amax, amax_lds[r * C::WAVES_N + w]);
+        const float sc = fmaxf(amax, kFp8Eps) / kFp8Max;
+        if (s >= row_end) continue;
+        uint8_t* q = p.act_q + static_cast<int64_t>(s) * p.N_act;
+#pragma unroll
+        for (int j = 0; j < NI / 2; ++j) {
+          const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2) + j * 16 + ocol;
+          uint32_t word = 0;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            word |= f32_to_e4m3(fminf(fmaxf(v[i][j][c] / sc, -kFp8Max), kFp8Max)) << (8 * c);
+          *reinterpret_cast<uint32_t*>(q + col) = word;
+        }
+        if (wn == 0 && ((lane >> 2) & 3) == 0) p.act_qs[static_cast<int64_t>(s) * ngrp + nt] = sc;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     const int s = row_beg + wm * WM + i * 16 + orow;

@@ -308,3 +308,27 @@ def test_tiny_decode_path_equals_aligned_path(M, fp8):
     ref = flaggems_sglang.triton_kernel_fused_experts(x, w13.transpose(1, 2), w2.transpose(1, 2),
                                                       rd, gi, si, **tkw)
     assert torch.equal(out, ref)
+
+
+# ------------------------------------------------------------ fused-path internals
+@pytest.mark.parametrize("M,on_input", [(256, False), (200, True), (1024, False)])
+def test_fp8_fused_act_quant_matches_stage_path(M, on_input):
+    """The fused fp8 prefill path quantizes the GEMM1 activation in the GEMM1
+    epilogue; the stage path (triton_kernel_fused_experts) runs the separate
+    fmoe_quant_fp8_group pass on the bf16 activation.  With N large enough
+    that GEMM2 splits K (fp32 partial planes in both paths) the two must agree
+    bit for bit."""
+    K, N, E, k = 512, 4096, 8, 2
+    d = O.make_inputs(M, K, N, E, k, wscale=0.02)
+    q1, s1 = Q.quantize_fp8_block(d["w13"].to(DEV))
+    q2, s2 = Q.quantize_fp8_block(d["w2"].to(DEV))
+    tw, ti = d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    x = d["x"].to(DEV)
+    fused = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, use_fp8_w8a8=True, w1_scale=s1, w2_scale=s2,
+                                          block_shape=[128, 128], apply_router_weight_on_input=on_input)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw, ti, E)
+    staged = flaggems_sglang.triton_kernel_fused_experts(
+        x, q1.transpose(1, 2), q2.transpose(1, 2), rd, gi, si, use_fp8_w8a8=True,
+        w1_scale=s1.transpose(1, 2), w2_scale=s2.transpose(1, 2), block_shape=[128, 128],
+        apply_router_weight_on_input=on_input)
+    assert torch.equal(fused, staged)
