@@ -332,3 +332,19 @@ def test_fp8_fused_act_quant_matches_stage_path(M, on_input):
         w1_scale=s1.transpose(1, 2), w2_scale=s2.transpose(1, 2), block_shape=[128, 128],
         apply_router_weight_on_input=on_input)
     assert torch.equal(fused, staged)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_int4_identity_expert_map_bit_exact(M):
+    """int4 decode with an identity expert map (the expert-parallel routing
+    path of fmoe_align_ex) equals the call without a map, bit for bit."""
+    K, N, E, k = 512, 384, 16, 4
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    q1, s1, z1 = Q.quantize_int4_group(d["w13"].to(DEV))
+    q2, s2, z2 = Q.quantize_int4_group(d["w2"].to(DEV))
+    args = (d["x"].to(DEV), q1, q2, d["topk_weights"].to(DEV), d["topk_ids"].to(DEV))
+    kw = dict(use_int4_w4a16=True, w1_scale=s1, w2_scale=s2, w1_zp=z1, w2_zp=z2)
+    plain = flaggems_sglang.fused_experts(*args, **kw)
+    emap = torch.arange(E, dtype=torch.int32, device=DEV)
+    mapped = flaggems_sglang.fused_experts(*args, expert_map=emap, global_num_experts=E, **kw)
+    assert torch.equal(plain, mapped)
