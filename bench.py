@@ -43,6 +43,9 @@ WORKLOADS = {
     "dsv3_fp8_m1": (1, 7168, 2048, 256, 8, "fp8", "grouped"),
     "mixtral_w4a16_m1": (1, 4096, 14336, 8, 2, "int4", "softmax"),
     "mixtral_w4a16_m16": (16, 4096, 14336, 8, 2, "int4", "softmax"),
+    # OCP MXFP4 weights (e2m1 + e8m0 per 32), bf16 activations
+    "mixtral_mxfp4_m1": (1, 4096, 14336, 8, 2, "mxfp4", "softmax"),
+    "mixtral_mxfp4_m16": (16, 4096, 14336, 8, 2, "mxfp4", "softmax"),
 }
 
 
@@ -61,6 +64,8 @@ def _gen_weights(E, R, C, gen, dev, wtype, chunk=8):
             outs.append((w,))
         elif wtype == "fp8":
             outs.append(Q.quantize_fp8_block(w))
+        elif wtype == "mxfp4":
+            outs.append(Q.quantize_mxfp4(w))
         else:
             outs.append(Q.quantize_int4_group(w))
         del w
@@ -93,6 +98,8 @@ def make_problem(name, seed=0):
         kw = dict(use_fp8_w8a8=True, w1_scale=w13[1], w2_scale=w2[1], block_shape=[128, 128])
     elif wtype == "int4":
         kw = dict(use_int4_w4a16=True, w1_scale=w13[1], w2_scale=w2[1], w1_zp=w13[2], w2_zp=w2[2])
+    elif wtype == "mxfp4":
+        kw = dict(use_mxfp4_w4a16=True, w1_scale=w13[1], w2_scale=w2[1])
     return dict(name=name, M=M, K=K, N=N, E=E, k=k, wtype=wtype, x=x, w13=w13[0], w2=w2[0],
                 tw=tw, ti=ti, kw=kw)
 
@@ -111,6 +118,8 @@ def weight_bytes_touched(p):
         per = 3 * K * N * 2
     elif p["wtype"] == "fp8":
         per = 3 * K * N + 4 * (2 * N // 128) * (K // 128) + 4 * (K // 128) * (N // 128)
+    elif p["wtype"] == "mxfp4":
+        per = 3 * K * N // 2 + 3 * K * N // 32
     else:
         per = 3 * K * N // 2 + 2 * (K // 128) * 2 * N + (K // 128) * N + 2 * (N // 128) * K + (N // 128) * K // 2
     return hit, hit * per
@@ -193,7 +202,7 @@ def stage_times(p, reps=10):
 
     L = _lib.lib()
     M, K, N, E, k = p["M"], p["K"], p["N"], p["E"], p["k"]
-    wt = {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4}[p["wtype"]]
+    wt = {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4, "mxfp4": _lib.W_MXFP4}[p["wtype"]]
     bm = L.fmoe_choose_block_m(wt, M, k, E, 0)
     kw = p["kw"]
     s13, s2 = kw.get("w1_scale"), kw.get("w2_scale")
@@ -294,7 +303,7 @@ def measure(name, steps, warmup):
     from flaggems_sglang import _lib
 
     p = make_problem(name)
-    wt = {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4}[p["wtype"]]
+    wt = {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4, "mxfp4": _lib.W_MXFP4}[p["wtype"]]
     decode = _lib.lib().fmoe_choose_block_m(wt, p["M"], p["k"], p["E"], 0) == 16
     timing = "wall clock per call, synchronous launches"
     if decode:
@@ -435,7 +444,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"bf16": "bf16", "fp8": "fp8-e4m3 (fp32 acc)", "int4": "int4 w / bf16 a"}[p["wtype"]],
+        "dtype": {"bf16": "bf16", "fp8": "fp8-e4m3 (fp32 acc)", "int4": "int4 w / bf16 a",
+                  "mxfp4": "mxfp4 w / bf16 a"}[p["wtype"]],
         "data": "synthetic: x~N(0,1), weights~N(0,0.02) random-init, router logits~N(0,1)",
         "config": {"workload": p["name"], "M": p["M"], "K": p["K"], "N": p["N"], "E": p["E"],
                    "top_k": p["k"], "weights": p["wtype"], "global_batch": p["M"],

@@ -23,10 +23,15 @@ constexpr int kPrefillTargetWgs = 6 * 256;
 
 size_t al(size_t v) { return (v + 255) & ~size_t(255); }
 
-bool valid_wtype(int wt) { return wt == FMOE_W_BF16 || wt == FMOE_W_FP8 || wt == FMOE_W_INT4; }
+bool valid_wtype(int wt) {
+  return wt == FMOE_W_BF16 || wt == FMOE_W_FP8 || wt == FMOE_W_INT4 || wt == FMOE_W_MXFP4;
+}
+// weight formats that only the streaming (decode) kernels read
+bool decode_only(int wt) { return wt == FMOE_W_INT4 || wt == FMOE_W_MXFP4; }
 
 WType to_wt(int wt) {
-  return wt == FMOE_W_FP8 ? WType::kFp8 : (wt == FMOE_W_INT4 ? WType::kInt4 : WType::kBf16);
+  return wt == FMOE_W_FP8 ? WType::kFp8
+                          : (wt == FMOE_W_INT4 ? WType::kInt4 : (wt == FMOE_W_MXFP4 ? WType::kMxfp4 : WType::kBf16));
 }
 
 int check_routing(const fmoe_routing* r, const char* who) {
@@ -71,7 +76,7 @@ GemmParams base_params(const fmoe_routing* r) {
 int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
   const int64_t slots = M * k;
   const int64_t active = slots < E ? slots : E;
-  if (wtype == FMOE_W_INT4 || path == 2) return kDecodeBM;
+  if (decode_only(wtype) || path == 2) return kDecodeBM;
   if (path != 1 && slots <= kDecodeBM * (active > 0 ? active : 1)) return kDecodeBM;
   const int64_t mean = slots / E;
   if (wtype == FMOE_W_BF16 && mean >= 256) return 256;
@@ -175,8 +180,10 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
     return fail(FMOE_ERR_INVALID, "gemm1: fp8 decode takes bf16 x (quantized in-kernel); x_scale must be null");
   if (wtype == FMOE_W_INT4 && (!w13_scale || !w13_zero))
     return fail(FMOE_ERR_INVALID, "gemm1: int4 needs w13_scale and w13_zero");
-  if (wtype == FMOE_W_INT4 && !is_decode(r))
-    return fail(FMOE_ERR_UNSUPPORTED, "gemm1: int4 weights need block_m=16 routing");
+  if (wtype == FMOE_W_MXFP4 && !w13_scale)
+    return fail(FMOE_ERR_INVALID, "gemm1: mxfp4 needs w13_scale (e8m0 block scales)");
+  if (decode_only(wtype) && !is_decode(r))
+    return fail(FMOE_ERR_UNSUPPORTED, "gemm1: int4 / mxfp4 weights need block_m=16 routing");
   if ((path == 1 && is_decode(r)) || (path == 2 && !is_decode(r)))
     return fail(FMOE_ERR_INVALID, "gemm1: path %d does not match block_m=%d", path, r->block_m);
   GemmParams p = base_params(r);
@@ -186,6 +193,7 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
   p.b_scale = static_cast<const float*>(w13_scale);
   p.b_gscale = static_cast<const uint16_t*>(w13_scale);
   p.b_zero = static_cast<const uint8_t*>(w13_zero);
+  p.b_mxscale = static_cast<const uint8_t*>(w13_scale);
   p.Kred = K;
   p.Nout = 2 * N;
   p.N_act = N;
@@ -241,8 +249,10 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
     return fail(FMOE_ERR_INVALID, "gemm2: fp8 decode takes bf16 act (quantized in-kernel); act_scale must be null");
   if (wtype == FMOE_W_INT4 && (!w2_scale || !w2_zero))
     return fail(FMOE_ERR_INVALID, "gemm2: int4 needs w2_scale and w2_zero");
-  if (wtype == FMOE_W_INT4 && !is_decode(r))
-    return fail(FMOE_ERR_UNSUPPORTED, "gemm2: int4 weights need block_m=16 routing");
+  if (wtype == FMOE_W_MXFP4 && !w2_scale)
+    return fail(FMOE_ERR_INVALID, "gemm2: mxfp4 needs w2_scale (e8m0 block scales)");
+  if (decode_only(wtype) && !is_decode(r))
+    return fail(FMOE_ERR_UNSUPPORTED, "gemm2: int4 / mxfp4 weights need block_m=16 routing");
   if ((path == 1 && is_decode(r)) || (path == 2 && !is_decode(r)))
     return fail(FMOE_ERR_INVALID, "gemm2: path %d does not match block_m=%d", path, r->block_m);
   if (splits < 1 || splits > 64)
@@ -254,6 +264,7 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
   p.b_scale = static_cast<const float*>(w2_scale);
   p.b_gscale = static_cast<const uint16_t*>(w2_scale);
   p.b_zero = static_cast<const uint8_t*>(w2_zero);
+  p.b_mxscale = static_cast<const uint8_t*>(w2_scale);
   p.Kred = N;
   p.Nout = K;
   p.N_act = N;
@@ -351,7 +362,7 @@ FusedLayout layout(const fmoe_fused_args* a) {
 // bf16 / fp8 only: for int4 the separate align launch measured faster (its
 // GEMMs are short enough that the in-workgroup routing latency shows).
 bool tiny_decode(const fmoe_fused_args* a, const FusedLayout& L) {
-  return L.bm == kDecodeBM && a->wtype != FMOE_W_INT4 && a->M <= 16 && a->M * a->top_k <= 512 &&
+  return L.bm == kDecodeBM && !decode_only(a->wtype) && a->M <= 16 && a->M * a->top_k <= 512 &&
          a->E <= 1024 && !a->expert_map;
 }
 
@@ -374,6 +385,7 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g1.b_scale = static_cast<const float*>(a->w13_scale);
   g1.b_gscale = static_cast<const uint16_t*>(a->w13_scale);
   g1.b_zero = static_cast<const uint8_t*>(a->w13_zero);
+  g1.b_mxscale = static_cast<const uint8_t*>(a->w13_scale);
   g1.Kred = a->K;
   g1.Nout = 2 * a->N;
   g1.N_act = a->N;
@@ -387,6 +399,7 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g2.b_scale = static_cast<const float*>(a->w2_scale);
   g2.b_gscale = static_cast<const uint16_t*>(a->w2_scale);
   g2.b_zero = static_cast<const uint8_t*>(a->w2_zero);
+  g2.b_mxscale = static_cast<const uint8_t*>(a->w2_scale);
   g2.Kred = a->N;
   g2.Nout = a->K;
   g2.N_act = a->N;

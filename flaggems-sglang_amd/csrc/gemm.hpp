@@ -16,6 +16,7 @@ struct GemmParams {
   const float* b_scale;    // fp8: [E, Nout/128, Kred/128]
   const uint16_t* b_gscale;  // int4: fp16 [E, Kred/128, Nout]
   const uint8_t* b_zero;   // int4: u4 [E, Kred/128, Nout/2]
+  const uint8_t* b_mxscale;  // mxfp4: e8m0 [E, Nout, Kred/32]
   int64_t Kred;            // reduction length (elements)
   int64_t Nout;            // weight rows per expert (GEMM1: 2N, GEMM2: K)
   int64_t N_act;           // GEMM1: N (columns of act)
@@ -58,7 +59,7 @@ struct GemmParams {
 enum Act { kActSilu = 0, kActGelu = 1, kActSwiglu = 2 };
 
 enum class Mode { kGemm1Silu, kGemm2 };
-enum class WType { kBf16, kFp8, kInt4 };
+enum class WType { kBf16, kFp8, kInt4, kMxfp4 };
 
 // Weight row of GEMM1 output column c: gate (u = 0) or up / linear (u = 1).
 // SiLU and GELU use split halves (gate c, up N + c), SWIGLU interleaved rows

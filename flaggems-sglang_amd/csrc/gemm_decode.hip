@@ -73,6 +73,13 @@ struct Stage<WType::kInt4> {
   uint8_t zb[NI];   // byte holding the group zero of this lane's column
 };
 
+template <>
+struct Stage<WType::kMxfp4> {
+  i32x4_t a[4];     // 32 bf16 of the activation row
+  i32x4_t b[NI];    // 32 e2m1 of each weight row (one 32-element scale block)
+  uint8_t sx[NI];   // e8m0 scale of that block
+};
+
 // Stages in flight per wave (see the file comment).
 constexpr int pipe_depth(WType wt, Mode mode) {
   return wt == WType::kFp8 && mode == Mode::kGemm1Silu ? 2 : 1;
@@ -191,16 +198,18 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 
   constexpr bool kFp8 = WT == WType::kFp8;
   constexpr bool kInt4 = WT == WType::kInt4;
+  constexpr bool kMx = WT == WType::kMxfp4;
+  constexpr bool kNib = kInt4 || kMx;  // 4-bit weights, two per byte
   // A rows: row lane%16 of the tile (bf16 for every format)
   const int s_a = slot_of((lane & 15) < n_rows ? (lane & 15) : 0);
   const int64_t a_row = MODE == Mode::kGemm1Silu ? (TINY ? s_a : p.topk_indx[s_a]) / p.top_k : s_a;
   const uint8_t* a_ptr = p.A + a_row * p.Kred * 2;
   // stage geometry
-  constexpr int kWStage = kInt4 ? 64 : 128;          // weight bytes per row per stage
-  constexpr int kElems = kInt4 ? 128 : (kFp8 ? 128 : 64);  // reduction elements per stage
-  const int64_t w_bytes = kInt4 ? p.Kred / 2 : (kFp8 ? p.Kred : p.Kred * 2);
+  constexpr int kWStage = kNib ? 64 : 128;          // weight bytes per row per stage
+  constexpr int kElems = kNib ? 128 : (kFp8 ? 128 : 64);  // reduction elements per stage
+  const int64_t w_bytes = kNib ? p.Kred / 2 : (kFp8 ? p.Kred : p.Kred * 2);
   const int nk = static_cast<int>(w_bytes / kWStage);
-  const int lane_off_w = (lane >> 4) * (kInt4 ? 16 : 32);
+  const int lane_off_w = (lane >> 4) * (kNib ? 16 : 32);
   const int lane_off_a = (lane >> 4) * (WT == WType::kBf16 ? 32 : 64);  // bf16 activations
 
   const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * w_bytes;
@@ -248,6 +257,16 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
       for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
 #pragma unroll
       for (int j = 0; j < NI; ++j) S.sb[j] = sb_ptr[j][kt];
+    } else if constexpr (kMx) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+      // this lane's 32 elements are scale block 4 kt + lane / 16 of its row
+      const int64_t nblk = p.Kred / 32;
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+        S.sx[j] = p.b_mxscale[(static_cast<int64_t>(e) * p.Nout + wrow[j]) * nblk + 4 * kt + (lane >> 4)];
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
@@ -319,6 +338,27 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
         t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, S.b[j], t, 0, 0, 0, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += t[r] * (sa[r] * S.sb[j]);
+      }
+    } else if constexpr (kMx) {
+      // e2m1 -> bf16 with the block scale folded in (hardware conversion,
+      // exact: e2m1 x 2^k fits bf16), then plain bf16 MFMAs.  Dword d of the
+      // lane's 16 bytes holds its elements 8d..8d+7, low nibble first -- the
+      // same order as the activations in S.a[d].
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const unsigned ex = S.sx[j];
+        const float sc = ex == 0 ? 0x1p-127f : (ex == 255 ? __builtin_nanf("") : __uint_as_float(ex << 23));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const unsigned wv = static_cast<unsigned>(S.b[j][d]);
+          const int b0 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wv, sc, 0));
+          const int b1 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wv, sc, 1));
+          const int b2 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wv, sc, 2));
+          const int b3 = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(wv, sc, 3));
+          const i32x4_t av = S.a[d];
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[0], av[1], av[2], av[3]),
+                                                           as_bf16x8(b0, b1, b2, b3), acc[j], 0, 0, 0);
+        }
       }
     } else {  // int4
       f32x4_t t[NI], xs = {0.f, 0.f, 0.f, 0.f};
@@ -445,7 +485,7 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
          static_cast<unsigned>(mode == Mode::kGemm2 ? p.splits : 1));
   dim3 b(decode::kThreads);
 #define LAUNCH(WT_, MODE_, ACT_)                                                                \
-  ((p.tiny_ids && WT_ != WType::kInt4)                                                          \
+  ((p.tiny_ids && WT_ != WType::kInt4 && WT_ != WType::kMxfp4)                              \
        ? decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, true><<<g, b, 0, s>>>(p) \
        : decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, false><<<g, b, 0, s>>>(p))
 #define LAUNCH_G1(WT_)                                                 \
@@ -457,12 +497,14 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
       case WType::kBf16: LAUNCH_G1(WType::kBf16); break;
       case WType::kFp8: LAUNCH_G1(WType::kFp8); break;
       case WType::kInt4: LAUNCH_G1(WType::kInt4); break;
+      case WType::kMxfp4: LAUNCH_G1(WType::kMxfp4); break;
     }
   } else {
     switch (wt) {
       case WType::kBf16: LAUNCH(WType::kBf16, Mode::kGemm2, kActSilu); break;
       case WType::kFp8: LAUNCH(WType::kFp8, Mode::kGemm2, kActSilu); break;
       case WType::kInt4: LAUNCH(WType::kInt4, Mode::kGemm2, kActSilu); break;
+      case WType::kMxfp4: LAUNCH(WType::kMxfp4, Mode::kGemm2, kActSilu); break;
     }
   }
 #undef LAUNCH_G1

@@ -20,12 +20,13 @@ from __future__ import annotations
 import ctypes
 import logging
 from dataclasses import dataclass, field
+from types import SimpleNamespace
 from typing import Optional
 
 import torch
 
 from .. import _lib
-from .._lib import W_BF16, W_FP8, W_INT4, check, lib, ptr, require_cuda, stream_of
+from .._lib import W_BF16, W_FP8, W_INT4, W_MXFP4, check, lib, ptr, require_cuda, stream_of
 
 logger = logging.getLogger(__name__)
 
@@ -242,10 +243,19 @@ def per_token_group_quant_fp8(x: torch.Tensor, group_size: int = 128):
 # GEMM stages over reference-format routing
 # ---------------------------------------------------------------------------
 def _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w1_zp, w2_zp,
-                     block_shape, per_channel_quant):
+                     block_shape, per_channel_quant, use_mxfp4_w4a16=False):
     assert per_channel_quant is False, _UNSUPPORTED_FEATURE_MSG.format(name="per_channel_quant")
-    if use_fp8_w8a8 and use_int4_w4a16:
-        raise ValueError("use_fp8_w8a8 and use_int4_w4a16 are exclusive")
+    if int(bool(use_fp8_w8a8)) + int(bool(use_int4_w4a16)) + int(bool(use_mxfp4_w4a16)) > 1:
+        raise ValueError("use_fp8_w8a8, use_int4_w4a16 and use_mxfp4_w4a16 are exclusive")
+    if use_mxfp4_w4a16:
+        assert block_shape is None or list(block_shape) in ([0, 32], [32]), \
+            _UNSUPPORTED_FEATURE_MSG.format(name=f"block_shape={block_shape}")
+        assert w1.dtype == torch.uint8 and w2.dtype == torch.uint8, "mxfp4 weights are packed uint8"
+        assert w1_scale is not None and w2_scale is not None, "mxfp4 needs w1_scale and w2_scale"
+        assert w1_scale.dtype in (torch.uint8, torch.float8_e8m0fnu) and \
+            w2_scale.dtype in (torch.uint8, torch.float8_e8m0fnu), "mxfp4 scales are e8m0 bytes"
+        assert w1_zp is None and w2_zp is None, _UNSUPPORTED_FEATURE_MSG.format(name="mxfp4 zero points")
+        return W_MXFP4
     if use_fp8_w8a8:
         assert block_shape is not None and list(block_shape) == [128, 128], \
             _UNSUPPORTED_FEATURE_MSG.format(name=f"block_shape={block_shape}")
@@ -288,7 +298,7 @@ def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens,
     fp32 biases (bias path)."""
     L = lib()
     M, K = x.shape
-    N = w2.shape[2] * (2 if wtype == W_INT4 else 1)
+    N = w2.shape[2] * (2 if wtype in (W_INT4, W_MXFP4) else 1)
     dev = x.device
     st = stream_of(x)
     r = _lib.Routing(ptr(topk_indx), ptr(gate_indx), ptr(gate_scal), ptr(offs_raw), ptr(offs_pad),
@@ -429,20 +439,34 @@ def triton_kernel_fused_experts_with_bias(
     ``act = g * sigmoid(alpha * g) * (l + 1)`` on the fp32 GEMM1 result, then
     the routing weight when applied on the input; GEMM2 adds ``b2`` before the
     routing weight.  ``gemm1_alpha=None`` means 1, ``gemm1_clamp_limit=None`` no
-    clamp.  Only bf16 weights (``w1_pcg`` / ``w2_pcg`` None).
+    clamp.
+
+    ``w1_pcg`` / ``w2_pcg`` (matmul_ogs precision configs): None for bf16
+    weights; for MXFP4 weights (OCP e2m1 + e8m0 block scales, W4A16) objects
+    whose ``weight_scale`` holds the block scales as plain row-major tensors,
+    ``[E, K/32, 2N]`` / ``[E, N/32, K]`` uint8 (or float8_e8m0fnu), with
+    ``w1 [E, K/2, 2N]`` / ``w2 [E, N/2, K]`` uint8 packed along the reduction
+    dim (low nibble = even element).  triton_kernels' swizzled value / scale
+    layouts are not accepted.
     """
     logger.debug("FLAGGEMS_SGLANG FUSED_MOE_WITH_BIAS")
     assert inplace is False, "Inplace is not supported"
     assert hidden_states.dtype == torch.bfloat16, "hidden_states must be bfloat16"
     if activation != "silu":
         raise ValueError(f"Unsupported FusedMoe activation: {activation}")
-    assert w1_pcg is None, _UNSUPPORTED_FEATURE_MSG.format(name="w1_pcg")
-    assert w2_pcg is None, _UNSUPPORTED_FEATURE_MSG.format(name="w2_pcg")
     assert hidden_states.ndim == 2, "hidden_states must be 2D"
-    assert w1.dtype == torch.bfloat16, "w1 must be bfloat16"
-    assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
-    assert hidden_states.shape[-1] == w1.shape[-2], "hidden size mismatch"
-    assert w2.shape[-1] == w1.shape[1], "intermediate size mismatch"
+    mx = w1_pcg is not None or w2_pcg is not None
+    if mx:
+        assert w1_pcg is not None and w2_pcg is not None, "w1_pcg and w2_pcg go together"
+        s1, s2 = _pcg_scale(w1_pcg, "w1_pcg"), _pcg_scale(w2_pcg, "w2_pcg")
+        assert w1.dtype == torch.uint8 and w2.dtype == torch.uint8, "mxfp4 weights are packed uint8"
+        Kh = w1.shape[1] * 2
+    else:
+        assert w1.dtype == torch.bfloat16, "w1 must be bfloat16"
+        assert w2.dtype == torch.bfloat16, "w2 must be bfloat16"
+        Kh = w1.shape[1]
+    assert hidden_states.shape[-1] == Kh, "hidden size mismatch"
+    assert w2.shape[-1] == Kh, "intermediate size mismatch"
     assert b1 is not None and b2 is not None, "Bias execution requires both w13_bias and w2_bias"
     E = routing_data.n_expts_tot
     assert tuple(b1.shape) == (E, w1.shape[2]) and tuple(b2.shape) == (E, w2.shape[2]), \
@@ -453,17 +477,34 @@ def triton_kernel_fused_experts_with_bias(
     k = routing_data.n_expts_act
     w13 = _as_sglang_layout(w1)
     w2t = _as_sglang_layout(w2)
-    bm = lib().fmoe_choose_block_m(_lib.W_BF16, M, k, E, 0)
+    wtype, s13, s2t = _lib.W_BF16, None, None
+    if mx:
+        wtype = W_MXFP4
+        s13, s2t = _as_sglang_layout(s1.view(torch.uint8)), _as_sglang_layout(s2.view(torch.uint8))
+        N2 = w13.shape[1]
+        assert tuple(s13.shape) == (E, N2, Kh // 32) and tuple(s2t.shape) == (E, Kh, w2t.shape[2] * 2 // 32), \
+            "mxfp4 scale shapes do not match the weights"
+        require_cuda(s13, s2t)
+    bm = lib().fmoe_choose_block_m(wtype, M, k, E, 0)
     offs_raw, offs_pad, tile_map, n_tiles = _expt_data_for(routing_data, M * k, bm)
     topk_indx = gather_indx.src_indx.to(torch.int32).contiguous()
     gate_indx = gather_indx.dst_indx.to(torch.int32).contiguous()
     gate_scal = routing_data.gate_scal.float().contiguous()
-    return _run_stages(x, w13, w2t, _lib.W_BF16, None, None, None, None, M, k, E, topk_indx,
+    return _run_stages(x, w13, w2t, wtype, s13, s2t, None, None, M, k, E, topk_indx,
                        gate_indx, gate_scal, offs_raw, offs_pad, tile_map, n_tiles, bm,
                        apply_router_weight_on_input, 1.0, combine=scatter_indx is not None,
                        act=_lib.ACT_SWIGLU, b13=b1.float().contiguous(), b2=b2.float().contiguous(),
                        alpha=1.0 if gemm1_alpha is None else float(gemm1_alpha),
                        limit=0.0 if gemm1_clamp_limit is None else float(gemm1_clamp_limit))
+
+
+def _pcg_scale(pcg, name):
+    """The MXFP4 block scales of a precision config (``weight_scale``)."""
+    sc = getattr(pcg, "weight_scale", None)
+    assert isinstance(sc, torch.Tensor), _UNSUPPORTED_FEATURE_MSG.format(
+        name=f"{name} without a plain weight_scale tensor")
+    assert sc.dtype in (torch.uint8, torch.float8_e8m0fnu), f"{name}.weight_scale must be e8m0 bytes"
+    return sc
 
 
 # ---------------------------------------------------------------------------
@@ -496,6 +537,7 @@ def fused_experts(
     path: int = 0,
     expert_map: Optional[torch.Tensor] = None,
     global_num_experts: int = -1,
+    use_mxfp4_w4a16: bool = False,
 ) -> torch.Tensor:
     """Whole fused MoE in one C call (align -> GEMM1+SiLU -> GEMM2 -> top-k sum).
 
@@ -506,7 +548,11 @@ def fused_experts(
       int4 (``use_int4_w4a16``, group 128): ``w1 [E, 2N, K/2]`` / ``w2 [E, K, N/2]``
            uint8 (two uint4 per byte, low nibble first), ``w1_scale [E, K/128, 2N]``
            / ``w2_scale [E, N/128, K]`` fp16, ``w1_zp [E, K/128, N]`` /
-           ``w2_zp [E, N/128, K/2]`` uint8 (two uint4 zeros per byte).
+           ``w2_zp [E, N/128, K/2]`` uint8 (two uint4 zeros per byte);
+      mxfp4 (``use_mxfp4_w4a16``): OCP MXFP4 ``w1 [E, 2N, K/2]`` / ``w2 [E, K, N/2]``
+           uint8 (two e2m1 per byte, low nibble first), ``w1_scale [E, 2N, K/32]`` /
+           ``w2_scale [E, K, N/32]`` e8m0 bytes; bf16 activations (the streaming
+           kernels, like int4).
     ``path``: 0 choose, 1 prefill kernels, 2 decode kernels.
     ``expert_map`` (expert parallel): ``topk_ids`` hold global expert ids,
     ``expert_map [global_num_experts]`` int maps each to a local expert (index
@@ -520,14 +566,19 @@ def fused_experts(
     assert hidden_states.ndim == 2 and hidden_states.dtype == torch.bfloat16, \
         "hidden_states must be 2D bfloat16"
     wtype = _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w1_zp,
-                             w2_zp, block_shape, per_channel_quant)
+                             w2_zp, block_shape, per_channel_quant, use_mxfp4_w4a16)
     require_cuda(hidden_states, w1, w2, topk_weights, topk_ids, w1_scale, w2_scale, w1_zp, w2_zp)
     x = hidden_states.contiguous()
     M, K = x.shape
     E = w1.shape[0]
     k = topk_ids.shape[1]
-    N = w2.shape[2] * (2 if wtype == W_INT4 else 1)
-    kin = w1.shape[2] * (2 if wtype == W_INT4 else 1)
+    nib = wtype in (W_INT4, W_MXFP4)
+    N = w2.shape[2] * (2 if nib else 1)
+    kin = w1.shape[2] * (2 if nib else 1)
+    if wtype == W_MXFP4:
+        assert tuple(w1_scale.shape) == (E, 2 * N, K // 32) and tuple(w2_scale.shape) == (E, K, N // 32), \
+            "mxfp4 scales must be [E, 2N, K/32] and [E, K, N/32]"
+        w1_scale, w2_scale = w1_scale.view(torch.uint8), w2_scale.view(torch.uint8)
     assert kin == K and w1.shape[1] == 2 * N and w2.shape[1] == K, "weight shapes do not match"
     for t in (w1, w2, w1_scale, w2_scale, w1_zp, w2_zp):
         if t is not None:
@@ -613,6 +664,10 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
         quant = dict(use_int4_w4a16=True, w1_scale=layer.w13_scales, w2_scale=layer.w2_scales,
                      w1_zp=layer.w13_qzeros, w2_zp=layer.w2_qzeros)
         w13, w2 = layer.w13_qweight, layer.w2_qweight
+    elif layer.w13_weight.dtype == torch.uint8 and getattr(layer, "w13_weight_scale", None) is not None:
+        # MXFP4 layer (SGLang Mxfp4 naming): e2m1 [E, 2N, K/2] + e8m0 [E, 2N, K/32]
+        quant = dict(use_mxfp4_w4a16=True, w1_scale=layer.w13_weight_scale, w2_scale=layer.w2_weight_scale)
+        w13, w2 = layer.w13_weight, layer.w2_weight
     elif getattr(layer, "w13_weight_scale_inv", None) is not None:
         quant = dict(use_fp8_w8a8=True, block_shape=[128, 128], w1_scale=layer.w13_weight_scale_inv,
                      w2_scale=layer.w2_weight_scale_inv)
@@ -622,16 +677,22 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
         w13, w2 = layer.w13_weight, layer.w2_weight
 
     if b13 is not None or b2 is not None:
-        # bias path (ops/fused_moe.py:364-383): fused swiglu, bf16 weights
+        # bias path (ops/fused_moe.py:364-383): fused swiglu, bf16 or MXFP4 weights
         assert b13 is not None and b2 is not None, "Bias execution requires both w13_bias and w2_bias"
-        assert not quant, _UNSUPPORTED_FEATURE_MSG.format(name="quantized weights with bias")
+        assert not quant or quant.get("use_mxfp4_w4a16"), \
+            _UNSUPPORTED_FEATURE_MSG.format(name="fp8 / int4 weights with bias")
+        pcg13 = pcg2 = None
+        if quant:
+            # matmul_ogs orientation views of the SGLang-layout scales (no copy)
+            pcg13 = SimpleNamespace(weight_scale=quant["w1_scale"].transpose(-1, -2))
+            pcg2 = SimpleNamespace(weight_scale=quant["w2_scale"].transpose(-1, -2))
         if isinstance(topk_output, tuple) and len(topk_output) == 3 and isinstance(topk_output[0], RoutingData):
             routing_data, gather_indx, scatter_indx = topk_output
         else:
             routing_data, gather_indx, scatter_indx = _standard_topk_to_triton_kernels(
                 topk_output.topk_weights, topk_output.topk_ids, cfg.num_experts)
         out = triton_kernel_fused_experts_with_bias(
-            hidden_states, w13.transpose(-1, -2), None, b13, w2.transpose(-1, -2), None, b2,
+            hidden_states, w13.transpose(-1, -2), pcg13, b13, w2.transpose(-1, -2), pcg2, b2,
             routing_data, gather_indx, None if no_combine else scatter_indx, activation=activation,
             apply_router_weight_on_input=on_input, gemm1_alpha=getattr(cfg, "gemm1_alpha", None),
             gemm1_clamp_limit=getattr(cfg, "gemm1_clamp_limit", None))

@@ -55,3 +55,34 @@ def quantize_int4_group(w: torch.Tensor, group: int = 128):
     q = torch.clamp(torch.round(wf / scf[..., None]) + z[..., None], 0, 15).to(torch.uint8)
     return (_pack_u4(q.view(E, R, C)), sc.transpose(1, 2).contiguous(),
             _pack_u4(z.to(torch.uint8).transpose(1, 2).contiguous()))
+
+
+_E2M1_CUTS = (0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0)
+
+
+def quantize_mxfp4(w: torch.Tensor, block: int = 32):
+    """OCP MXFP4 quantization of ``w [E, R, C]`` along C (the reduction dim):
+    one e8m0 scale per 32 elements with the RCEIL rule of torch's reference
+    MX quantizer (exponent = ceil(log2(amax / 6)), clamped to [-127, 127]; no
+    element saturates), elements rounded to E2M1 (nearest, ties to the even
+    code).  Returns ``(qweight [E, R, C/2] u8, scales [E, R, C/32] u8)``, two
+    elements per byte, low nibble first."""
+    E, R, C = w.shape
+    if C % block:
+        raise ValueError(f"quantize_mxfp4: {C} is not a multiple of {block}")
+    g = w.float().view(E, R, C // block, block)
+    amax = g.abs().amax(dim=-1)
+    ex = torch.ceil(torch.log2(amax / torch.full_like(amax, 6.0)))
+    ex = torch.where(torch.isfinite(ex), ex, torch.full_like(ex, -127.0)).clamp(-127, 127)
+    scale = (ex + 127).to(torch.uint8)
+    inv = torch.where(scale == 0, torch.ones_like(ex), torch.exp2(-ex))
+    a = g * inv[..., None]
+    m = a.abs()
+    # code = number of E2M1 decision points passed; ties go to the even code
+    c = torch.zeros_like(m, dtype=torch.uint8)
+    for i, cut in enumerate(_E2M1_CUTS):
+        passed = (m >= cut) if i % 2 == 1 else (m > cut)
+        c = torch.where(passed, torch.full_like(c, i + 1), c)
+    c = c | (torch.signbit(a).to(torch.uint8) << 3)
+    c = c.view(E, R, C)
+    return (c[..., 0::2] | (c[..., 1::2] << 4)).contiguous(), scale.contiguous()

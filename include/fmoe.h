@@ -46,6 +46,10 @@ enum fmoe_wtype {
   FMOE_W_BF16 = 0,     /* bf16 weights, bf16 activations */
   FMOE_W_FP8 = 1,      /* fp8 e4m3fn weights with 128x128 block scales, 1x128 dynamic activation quant */
   FMOE_W_INT4 = 2,     /* uint4 weights with fp16 group scales and uint4 zeros, bf16 activations */
+  FMOE_W_MXFP4 = 3,    /* OCP MXFP4 weights (e2m1, one e8m0 scale per 32 along the reduction
+                          dim), bf16 activations: w13 [E, 2N, K/2] u8 + scale [E, 2N, K/32] u8,
+                          w2 [E, K, N/2] u8 + scale [E, K, N/32] u8; element 2i in the low
+                          nibble; w = e2m1(q) * 2^(s - 127) */
 };
 
 /* GEMM1 activations (the fused epilogue of fmoe_gemm1_ex / fmoe_fused_experts). */

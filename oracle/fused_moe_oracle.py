@@ -55,6 +55,14 @@ fused_experts_bias             fp64 per-token brute force; zero weights reduce
                                to sum_j w_j b2[e_j] (closed form).  The order
                                bias -> activation -> routing weight inside
                                matmul_ogs is *unpinned* (external code).
+mxfp4_quant / mxfp4_dequant    torch's reference MX quantizer
+                               (``torch.testing._internal.common_quantized.
+                               to_mxfp``, RCEIL scale rule) bit for bit; the
+                               OCP E2M1 table (16 codes) and tie / saturation
+                               known answers; the MI355X hardware conversion
+                               ``v_cvt_scalef32_pk_bf16_fp4`` (GPU test).  The
+                               MXFP4 MoE GEMM itself = the bf16 path on
+                               dequantized weights (pinned as above).
 per_token_group_quant_fp8      torch ``float8_e4m3fn`` cast; exact powers of 2;
                                amax element maps to +-448 exactly
 block_quant_fp8                same; dequant round-trip error bound
@@ -616,3 +624,84 @@ def make_inputs(M, K, N, E, topk, wscale=0.02, seed=None, routing="softmax",
     else:
         tw, ti = grouped_topk(logits, topk, n_group, topk_group)
     return dict(x=x, w13=w13, w2=w2, logits=logits, topk_weights=tw, topk_ids=ti)
+
+
+# --------------------------------------------------------------------------
+# MXFP4 weights (OCP Microscaling Formats v1.0: E2M1 elements, one E8M0
+# scale per 32 consecutive elements along the reduction dim).  The reference
+# passes such weights to matmul_ogs through ``w1_pcg`` / ``w2_pcg``
+# (ops/fused_moe.py:219-309, :374-378) with bf16 activations (W4A16).
+# --------------------------------------------------------------------------
+E2M1_VALUES = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], dtype=np.float32)
+
+
+def e2m1_encode(v: np.ndarray) -> np.ndarray:
+    """fp32 -> E2M1 code (bit 3 = sign): round to nearest, ties to the even
+    code, saturating at 6."""
+    a = np.abs(v.astype(np.float32))
+    c = np.zeros(a.shape, dtype=np.uint8)
+    c = np.where(a > 0.25, 1, c)
+    c = np.where(a >= 0.75, 2, c)
+    c = np.where(a > 1.25, 3, c)
+    c = np.where(a >= 1.75, 4, c)
+    c = np.where(a > 2.5, 5, c)
+    c = np.where(a >= 3.5, 6, c)
+    c = np.where(a > 5.0, 7, c)
+    return (c | (np.signbit(v).astype(np.uint8) << 3)).astype(np.uint8)
+
+
+def e2m1_decode(c: np.ndarray) -> np.ndarray:
+    v = E2M1_VALUES[c & 7]
+    return np.where(c & 8, -v, v).astype(np.float32)
+
+
+def e8m0_value(s: np.ndarray) -> np.ndarray:
+    """E8M0 scale byte -> 2^(s - 127) (255 = NaN)."""
+    s = s.astype(np.int32)
+    return np.where(s == 255, np.nan, np.ldexp(np.float32(1.0), s - 127)).astype(np.float32)
+
+
+def mxfp4_quant(w: torch.Tensor, block: int = 32):
+    """``w [..., C]`` (bf16) -> (packed e2m1 ``[..., C/2]`` u8, element 2i in the
+    low nibble; e8m0 scales ``[..., C/32]`` u8), with the scale rule of torch's
+    reference MX quantizer (RCEIL): exponent = ceil(log2(amax / 6)) clamped to
+    [-127, 127], so no element saturates, and elements x * 2^-exponent rounded
+    to E2M1 (nearest, ties to even)."""
+    wf = w.float().numpy()
+    *lead, C = wf.shape
+    g = wf.reshape(*lead, C // block, block)
+    amax = np.abs(g).max(axis=-1)
+    with np.errstate(divide="ignore"):
+        ex = np.ceil(np.log2(amax / np.float32(6.0)))
+    ex = np.clip(np.where(np.isfinite(ex), ex, -127), -127, 127).astype(np.int32)
+    s = (ex + 127).astype(np.uint8)
+    inv = np.where(s == 0, np.float32(1.0), np.ldexp(np.float32(1.0), -ex)).astype(np.float32)
+    codes = e2m1_encode(g * inv[..., None]).reshape(*lead, C)
+    packed = (codes[..., 0::2] | (codes[..., 1::2] << 4)).astype(np.uint8)
+    return torch.from_numpy(packed), torch.from_numpy(s)
+
+
+def mxfp4_dequant(packed: torch.Tensor, scales: torch.Tensor, block: int = 32) -> torch.Tensor:
+    """Inverse layout of ``mxfp4_quant``: value = e2m1 * 2^(scale - 127), fp32."""
+    p = packed.numpy()
+    codes = np.empty((*p.shape[:-1], p.shape[-1] * 2), dtype=np.uint8)
+    codes[..., 0::2] = p & 15
+    codes[..., 1::2] = p >> 4
+    v = e2m1_decode(codes)
+    sv = np.repeat(e8m0_value(scales.numpy()), block, axis=-1)
+    return torch.from_numpy(v * sv)
+
+
+def fused_experts_mxfp4(x, w13_q, w13_s, w2_q, w2_s, topk_weights, topk_ids,
+                        routed_scaling_factor=None, apply_router_weight_on_input=False,
+                        activation="silu"):
+    """MXFP4 weights (SGLang layout, ``[E, rows, K/2]`` + ``[E, rows, K/32]``),
+    bf16 activations: the bf16 fused_experts semantics on dequantized weights."""
+    E = w13_q.shape[0]
+    return fused_experts(
+        x, None, None, topk_weights, topk_ids,
+        apply_router_weight_on_input=apply_router_weight_on_input,
+        routed_scaling_factor=routed_scaling_factor, activation=activation,
+        w13_deq=_Deq(lambda e: mxfp4_dequant(w13_q[e], w13_s[e]), E),
+        w2_deq=_Deq(lambda e: mxfp4_dequant(w2_q[e], w2_s[e]), E),
+    )

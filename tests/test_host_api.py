@@ -73,8 +73,11 @@ def test_bias_path_argument_checks():
         f(x, w1, None, b1, w2, None, b2, rd, None, None, inplace=True)
     with pytest.raises(ValueError, match="Unsupported FusedMoe activation: gelu"):
         f(x, w1, None, b1, w2, None, b2, rd, None, None, activation="gelu")
-    with pytest.raises(AssertionError, match="w1_pcg is not supported"):
+    with pytest.raises(AssertionError, match="go together"):
         f(x, w1, object(), b1, w2, None, b2, rd, None, None)
+    # precision configs must carry plain MXFP4 block scales
+    with pytest.raises(AssertionError, match="w1_pcg without a plain weight_scale tensor is not supported"):
+        f(x, w1, object(), b1, w2, object(), b2, rd, None, None)
     with pytest.raises(AssertionError, match="requires both"):
         f(x, w1, None, b1, w2, None, None, rd, None, None)
     with pytest.raises(ValueError, match="GPU"):
