@@ -658,7 +658,8 @@ def e2m1_decode(c: np.ndarray) -> np.ndarray:
 def e8m0_value(s: np.ndarray) -> np.ndarray:
     """E8M0 scale byte -> 2^(s - 127) (255 = NaN)."""
     s = s.astype(np.int32)
-    return np.where(s == 255, np.nan, np.ldexp(np.float32(1.0), s - 127)).astype(np.float32)
+    v = np.ldexp(np.float32(1.0), np.minimum(s, 254) - 127)  # 255 (NaN) handled below
+    return np.where(s == 255, np.float32(np.nan), v).astype(np.float32)
 
 
 def mxfp4_quant(w: torch.Tensor, block: int = 32):
