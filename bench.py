@@ -193,8 +193,12 @@ def time_op_graph(p, steps, min_bytes=2e9):
 
 
 def stage_times(p, reps=10):
-    """Per-stage device time (ms) of one fused call, from HIP events recorded on
-    the launch stream around each C-ABI stage (same kernels as the fused call)."""
+    """Per-stage device time (ms) through the stage-level C ABI (align, quant,
+    GEMM1, quant, GEMM2, moe_sum), from HIP events recorded on the launch
+    stream around each call.  The fused call runs the same GEMM kernels but
+    folds two steps: on the fp8 prefill path the GEMM1 epilogue quantizes the
+    activation (no separate quant_act pass), and without split-K its GEMM2
+    rows are bf16 (halving the moe_sum read)."""
     import torch
 
     from flaggems_sglang import _lib
