@@ -1,0 +1,152 @@
+"""Edge shapes and HIP-graph capture of the fused op (all weight formats).
+
+Edge cases: no tokens, one expert with top-1, the minimum K = N = 128, every
+token routed to the same expert (one expert, many tiles), top-k equal to the
+expert count, and rows of exact zeros.  Graphs: ``fused_experts`` captured in
+a HIP graph and replayed several times, with eager work and synchronizations
+between the replays; every replay must equal the eager result bit for bit
+(the kernels allocate nothing and issue no memsets, so a capture is legal).
+"""
+
+import pytest
+import torch
+
+import flaggems_sglang
+from flaggems_sglang import quant as Q
+from oracle import fused_moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+FORMATS = ["bf16", "fp8", "int4", "mxfp4"]
+
+
+def _weights(fmt, d):
+    w13, w2 = d["w13"].to(DEV), d["w2"].to(DEV)
+    if fmt == "bf16":
+        return w13, w2, {}
+    if fmt == "fp8":
+        q1, s1 = Q.quantize_fp8_block(w13)
+        q2, s2 = Q.quantize_fp8_block(w2)
+        return q1, q2, dict(use_fp8_w8a8=True, w1_scale=s1, w2_scale=s2, block_shape=[128, 128])
+    if fmt == "int4":
+        q1, s1, z1 = Q.quantize_int4_group(w13)
+        q2, s2, z2 = Q.quantize_int4_group(w2)
+        return q1, q2, dict(use_int4_w4a16=True, w1_scale=s1, w2_scale=s2, w1_zp=z1, w2_zp=z2)
+    q1, s1 = Q.quantize_mxfp4(w13)
+    q2, s2 = Q.quantize_mxfp4(w2)
+    return q1, q2, dict(use_mxfp4_w4a16=True, w1_scale=s1, w2_scale=s2)
+
+
+def _oracle(fmt, d, q1, q2, kw):
+    args = (d["topk_weights"], d["topk_ids"])
+    if fmt == "bf16":
+        return O.fused_experts(d["x"], d["w13"], d["w2"], *args)
+    if fmt == "fp8":
+        return O.fused_experts_fp8(d["x"], q1.cpu(), kw["w1_scale"].cpu(), q2.cpu(), kw["w2_scale"].cpu(), *args)
+    if fmt == "int4":
+        return O.fused_experts_w4a16(d["x"], q1.cpu(), kw["w1_scale"].cpu(), kw["w1_zp"].cpu(), q2.cpu(),
+                                     kw["w2_scale"].cpu(), kw["w2_zp"].cpu(), *args)
+    return O.fused_experts_mxfp4(d["x"], q1.cpu(), kw["w1_scale"].cpu(), q2.cpu(), kw["w2_scale"].cpu(), *args)
+
+
+def _close(out, ref, tol, flip=1.0):
+    """|out - ref| <= flip * tol * rms(ref) + tol * |ref| elementwise and a
+    global relative error below tol / 4.  ``flip`` widens the absolute part
+    where rounding flips concentrate: the fp8 path quantizes the intermediate
+    activation to e4m3 (3 mantissa bits), so an element sitting on a rounding
+    boundary can land on the neighbouring code on either side, moving every
+    output of its token by up to 1/8 of that element's contribution; with all
+    tokens on the same expert pair the same weight columns amplify each flip."""
+    out = out.float().cpu()
+    ref = ref.float()
+    scale = max(float(ref.pow(2).mean().sqrt()), 1e-3) if ref.numel() else 1.0
+    torch.testing.assert_close(out, ref, atol=flip * tol * scale, rtol=tol)
+    if ref.numel() and float(ref.norm()) > 0:
+        rel = float((out - ref).norm() / ref.norm())
+        assert rel < tol / 4, f"global relative error {rel:.3e}"
+
+
+def _run(d, q1, q2, kw, **extra):
+    return flaggems_sglang.fused_experts(d["x"].to(DEV), q1, q2, d["topk_weights"].to(DEV),
+                                         d["topk_ids"].to(DEV), **kw, **extra)
+
+
+def _staged_fp8(d, q1, q2, kw):
+    """The same layer through the routing-data entry, which quantizes the
+    intermediate activation in a pass of its own."""
+    from flaggems_sglang.ops.fused_moe import _standard_topk_to_triton_kernels
+    E = q1.shape[0]
+    rd, gi, si = _standard_topk_to_triton_kernels(d["topk_weights"].to(DEV), d["topk_ids"].to(DEV), E)
+    return flaggems_sglang.triton_kernel_fused_experts(
+        d["x"].to(DEV), q1.transpose(1, 2), q2.transpose(1, 2), rd, gi, si, use_fp8_w8a8=True,
+        w1_scale=kw["w1_scale"].transpose(1, 2), w2_scale=kw["w2_scale"].transpose(1, 2),
+        block_shape=[128, 128])
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("case", ["no_tokens", "one_expert_top1", "min_dims", "all_to_one_expert",
+                                  "topk_equals_E", "zero_rows"])
+def test_edge_shapes(fmt, case):
+    tol = 2e-2 if fmt in ("bf16", "mxfp4") else 5e-2
+    if case == "no_tokens":
+        d = O.make_inputs(1, 256, 256, 4, 2, wscale=0.05)
+        q1, q2, kw = _weights(fmt, d)
+        out = flaggems_sglang.fused_experts(torch.empty(0, 256, dtype=torch.bfloat16, device=DEV), q1, q2,
+                                            torch.empty(0, 2, device=DEV),
+                                            torch.empty(0, 2, dtype=torch.int32, device=DEV), **kw)
+        assert out.shape == (0, 256)
+        return
+    if case == "one_expert_top1":
+        d = O.make_inputs(37, 256, 256, 1, 1, wscale=0.05)
+    elif case == "min_dims":
+        d = O.make_inputs(70, 128, 128, 4, 2, wscale=0.05)
+    elif case == "all_to_one_expert":
+        d = O.make_inputs(300, 256, 256, 8, 2, wscale=0.05)
+        d["topk_ids"] = torch.stack([torch.full((300,), 5), torch.full((300,), 2)], 1).to(torch.int32)
+    elif case == "topk_equals_E":
+        d = O.make_inputs(20, 256, 256, 4, 4, wscale=0.05)
+    else:
+        d = O.make_inputs(40, 256, 256, 8, 2, wscale=0.05)
+        d["x"][::3] = 0
+    q1, q2, kw = _weights(fmt, d)
+    out = _run(d, q1, q2, kw)
+    concentrated = fmt == "fp8" and case == "all_to_one_expert"
+    _close(out, _oracle(fmt, d, q1, q2, kw), tol, flip=2.0 if concentrated else 1.0)
+    if concentrated:
+        # the fused path (activation quantized in the GEMM1 epilogue) against
+        # the staged path (separate quantization pass) on the same inputs
+        staged = _staged_fp8(d, q1, q2, kw)
+        torch.testing.assert_close(out.float(), staged.float(), atol=tol * 0.25, rtol=2 ** -7)
+    if case == "zero_rows":
+        assert torch.count_nonzero(out[::3]) == 0
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+@pytest.mark.parametrize("M", [3, 300])
+def test_graph_replays_equal_eager(fmt, M):
+    d = O.make_inputs(M, 512, 384, 8, 2, wscale=0.05)
+    q1, q2, kw = _weights(fmt, d)
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+
+    def op():
+        return flaggems_sglang.fused_experts(x, q1, q2, tw, ti, **kw)
+
+    eager = op()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        op()  # warm the workspace cache outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = op()
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        # unrelated eager work between replays
+        _ = (torch.randn(1024, 1024, device=DEV) @ torch.randn(1024, 1024, device=DEV)).sum().item()
+        assert torch.equal(op(), eager)
