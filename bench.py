@@ -43,10 +43,20 @@ WORKLOADS = {
     "dsv3_fp8_m1": (1, 7168, 2048, 256, 8, "fp8", "grouped"),
     "mixtral_w4a16_m1": (1, 4096, 14336, 8, 2, "int4", "softmax"),
     "mixtral_w4a16_m16": (16, 4096, 14336, 8, 2, "int4", "softmax"),
+    # the same int4 weights tiled at load time (quant.tile_int4)
+    "mixtral_w4a16t_m1": (1, 4096, 14336, 8, 2, "int4t", "softmax"),
+    "mixtral_w4a16t_m16": (16, 4096, 14336, 8, 2, "int4t", "softmax"),
     # OCP MXFP4 weights (e2m1 + e8m0 per 32), bf16 activations
     "mixtral_mxfp4_m1": (1, 4096, 14336, 8, 2, "mxfp4", "softmax"),
     "mixtral_mxfp4_m16": (16, 4096, 14336, 8, 2, "mxfp4", "softmax"),
 }
+
+
+def _wt_codes():
+    from flaggems_sglang import _lib
+
+    return {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4, "int4t": _lib.W_INT4_TILED,
+            "mxfp4": _lib.W_MXFP4}
 
 
 def _gen_weights(E, R, C, gen, dev, wtype, chunk=8):
@@ -69,9 +79,10 @@ def _gen_weights(E, R, C, gen, dev, wtype, chunk=8):
         else:
             outs.append(Q.quantize_int4_group(w))
         del w
-    if wtype == "int4":
+    if wtype in ("int4", "int4t"):
         # scales / zeros are [E, G, R]: concatenate along experts as well
-        return tuple(torch.cat([o[i] for o in outs]) for i in range(3))
+        q, sc, z = (torch.cat([o[i] for o in outs]) for i in range(3))
+        return (Q.tile_int4(q) if wtype == "int4t" else q), sc, z
     return tuple(torch.cat([o[i] for o in outs]) for i in range(len(outs[0])))
 
 
@@ -96,7 +107,7 @@ def make_problem(name, seed=0):
     kw = {}
     if wtype == "fp8":
         kw = dict(use_fp8_w8a8=True, w1_scale=w13[1], w2_scale=w2[1], block_shape=[128, 128])
-    elif wtype == "int4":
+    elif wtype in ("int4", "int4t"):
         kw = dict(use_int4_w4a16=True, w1_scale=w13[1], w2_scale=w2[1], w1_zp=w13[2], w2_zp=w2[2])
     elif wtype == "mxfp4":
         kw = dict(use_mxfp4_w4a16=True, w1_scale=w13[1], w2_scale=w2[1])
@@ -120,7 +131,7 @@ def weight_bytes_touched(p):
         per = 3 * K * N + 4 * (2 * N // 128) * (K // 128) + 4 * (K // 128) * (N // 128)
     elif p["wtype"] == "mxfp4":
         per = 3 * K * N // 2 + 3 * K * N // 32
-    else:
+    else:  # int4, row-major or tiled
         per = 3 * K * N // 2 + 2 * (K // 128) * 2 * N + (K // 128) * N + 2 * (N // 128) * K + (N // 128) * K // 2
     return hit, hit * per
 
@@ -206,7 +217,7 @@ def stage_times(p, reps=10):
 
     L = _lib.lib()
     M, K, N, E, k = p["M"], p["K"], p["N"], p["E"], p["k"]
-    wt = {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4, "mxfp4": _lib.W_MXFP4}[p["wtype"]]
+    wt = _wt_codes()[p["wtype"]]
     bm = L.fmoe_choose_block_m(wt, M, k, E, 0)
     kw = p["kw"]
     s13, s2 = kw.get("w1_scale"), kw.get("w2_scale")
@@ -307,7 +318,7 @@ def measure(name, steps, warmup):
     from flaggems_sglang import _lib
 
     p = make_problem(name)
-    wt = {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4, "mxfp4": _lib.W_MXFP4}[p["wtype"]]
+    wt = _wt_codes()[p["wtype"]]
     decode = _lib.lib().fmoe_choose_block_m(wt, p["M"], p["k"], p["E"], 0) == 16
     timing = "wall clock per call, synchronous launches"
     if decode:
@@ -336,7 +347,7 @@ def roofline_gemm1(res):
     if decode:
         hit = res["experts_hit"]
         K, N = p["K"], p["N"]
-        if p["wtype"] == "int4":
+        if p["wtype"] in ("int4", "int4t"):
             wb = 2 * N * K // 2 + 2 * (K // 128) * 2 * N + (K // 128) * N
         elif p["wtype"] == "fp8":
             wb = 2 * N * K + 4 * (2 * N // 128) * (K // 128)
@@ -418,7 +429,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="mixtral_bf16_m4096", choices=sorted(WORKLOADS))
-    ap.add_argument("--secondary", default="dsv3_fp8_m4096,mixtral_w4a16_m1,mixtral_w4a16_m16",
+    ap.add_argument("--secondary", default="dsv3_fp8_m4096,mixtral_w4a16t_m1,mixtral_w4a16t_m16,"
+                                           "mixtral_w4a16_m1,mixtral_w4a16_m16",
                     help="comma list of extra workloads reported in 'secondary' ('' for none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calib", action="store_true",
@@ -449,7 +461,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": {"bf16": "bf16", "fp8": "fp8-e4m3 (fp32 acc)", "int4": "int4 w / bf16 a",
-                  "mxfp4": "mxfp4 w / bf16 a"}[p["wtype"]],
+                  "int4t": "int4 w (tiled) / bf16 a", "mxfp4": "mxfp4 w / bf16 a"}[p["wtype"]],
         "data": "synthetic: x~N(0,1), weights~N(0,0.02) random-init, router logits~N(0,1)",
         "config": {"workload": p["name"], "M": p["M"], "K": p["K"], "N": p["N"], "E": p["E"],
                    "top_k": p["k"], "weights": p["wtype"], "global_batch": p["M"],

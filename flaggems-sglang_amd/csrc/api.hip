@@ -24,14 +24,16 @@ constexpr int kPrefillTargetWgs = 6 * 256;
 size_t al(size_t v) { return (v + 255) & ~size_t(255); }
 
 bool valid_wtype(int wt) {
-  return wt == FMOE_W_BF16 || wt == FMOE_W_FP8 || wt == FMOE_W_INT4 || wt == FMOE_W_MXFP4;
+  return wt == FMOE_W_BF16 || wt == FMOE_W_FP8 || wt == FMOE_W_INT4 || wt == FMOE_W_MXFP4 ||
+         wt == FMOE_W_INT4_TILED;
 }
 // weight formats that only the streaming (decode) kernels read
-bool decode_only(int wt) { return wt == FMOE_W_INT4 || wt == FMOE_W_MXFP4; }
+bool is_int4(int wt) { return wt == FMOE_W_INT4 || wt == FMOE_W_INT4_TILED; }
+bool decode_only(int wt) { return is_int4(wt) || wt == FMOE_W_MXFP4; }
 
 WType to_wt(int wt) {
   return wt == FMOE_W_FP8 ? WType::kFp8
-                          : (wt == FMOE_W_INT4 ? WType::kInt4 : (wt == FMOE_W_MXFP4 ? WType::kMxfp4 : WType::kBf16));
+                          : (is_int4(wt) ? WType::kInt4 : (wt == FMOE_W_MXFP4 ? WType::kMxfp4 : WType::kBf16));
 }
 
 int check_routing(const fmoe_routing* r, const char* who) {
@@ -178,7 +180,7 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
     return fail(FMOE_ERR_INVALID, "gemm1: fp8 prefill needs pre-quantized x with x_scale");
   if (wtype == FMOE_W_FP8 && is_decode(r) && x_scale)
     return fail(FMOE_ERR_INVALID, "gemm1: fp8 decode takes bf16 x (quantized in-kernel); x_scale must be null");
-  if (wtype == FMOE_W_INT4 && (!w13_scale || !w13_zero))
+  if (is_int4(wtype) && (!w13_scale || !w13_zero))
     return fail(FMOE_ERR_INVALID, "gemm1: int4 needs w13_scale and w13_zero");
   if (wtype == FMOE_W_MXFP4 && !w13_scale)
     return fail(FMOE_ERR_INVALID, "gemm1: mxfp4 needs w13_scale (e8m0 block scales)");
@@ -194,6 +196,7 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
   p.b_gscale = static_cast<const uint16_t*>(w13_scale);
   p.b_zero = static_cast<const uint8_t*>(w13_zero);
   p.b_mxscale = static_cast<const uint8_t*>(w13_scale);
+  p.b_tiled = wtype == FMOE_W_INT4_TILED;
   p.Kred = K;
   p.Nout = 2 * N;
   p.N_act = N;
@@ -247,7 +250,7 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
     return fail(FMOE_ERR_INVALID, "gemm2: fp8 prefill needs pre-quantized act with act_scale");
   if (wtype == FMOE_W_FP8 && is_decode(r) && act_scale)
     return fail(FMOE_ERR_INVALID, "gemm2: fp8 decode takes bf16 act (quantized in-kernel); act_scale must be null");
-  if (wtype == FMOE_W_INT4 && (!w2_scale || !w2_zero))
+  if (is_int4(wtype) && (!w2_scale || !w2_zero))
     return fail(FMOE_ERR_INVALID, "gemm2: int4 needs w2_scale and w2_zero");
   if (wtype == FMOE_W_MXFP4 && !w2_scale)
     return fail(FMOE_ERR_INVALID, "gemm2: mxfp4 needs w2_scale (e8m0 block scales)");
@@ -265,6 +268,7 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
   p.b_gscale = static_cast<const uint16_t*>(w2_scale);
   p.b_zero = static_cast<const uint8_t*>(w2_zero);
   p.b_mxscale = static_cast<const uint8_t*>(w2_scale);
+  p.b_tiled = wtype == FMOE_W_INT4_TILED;
   p.Kred = N;
   p.Nout = K;
   p.N_act = N;
@@ -301,7 +305,7 @@ int check_fused(const fmoe_fused_args* a) {
   if (a->K <= 0 || a->N <= 0 || a->K % 128 != 0 || a->N % 128 != 0)
     return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: K=%lld N=%lld must be multiples of 128",
                 static_cast<long long>(a->K), static_cast<long long>(a->N));
-  if (a->wtype == FMOE_W_INT4 && a->group_size != 128)
+  if (is_int4(a->wtype) && a->group_size != 128)
     return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: int4 group_size=%d is not supported",
                 a->group_size);
   if (a->path < 0 || a->path > 2) return fail(FMOE_ERR_INVALID, "fused_experts: path %d", a->path);
@@ -386,6 +390,7 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g1.b_gscale = static_cast<const uint16_t*>(a->w13_scale);
   g1.b_zero = static_cast<const uint8_t*>(a->w13_zero);
   g1.b_mxscale = static_cast<const uint8_t*>(a->w13_scale);
+  g1.b_tiled = a->wtype == FMOE_W_INT4_TILED;
   g1.Kred = a->K;
   g1.Nout = 2 * a->N;
   g1.N_act = a->N;
@@ -400,6 +405,7 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g2.b_gscale = static_cast<const uint16_t*>(a->w2_scale);
   g2.b_zero = static_cast<const uint8_t*>(a->w2_zero);
   g2.b_mxscale = static_cast<const uint8_t*>(a->w2_scale);
+  g2.b_tiled = a->wtype == FMOE_W_INT4_TILED;
   g2.Kred = a->N;
   g2.Nout = a->K;
   g2.N_act = a->N;

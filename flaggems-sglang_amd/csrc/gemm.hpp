@@ -17,6 +17,8 @@ struct GemmParams {
   const uint16_t* b_gscale;  // int4: fp16 [E, Kred/128, Nout]
   const uint8_t* b_zero;   // int4: u4 [E, Kred/128, Nout/2]
   const uint8_t* b_mxscale;  // mxfp4: e8m0 [E, Nout, Kred/32]
+  int b_tiled;             // int4: B in the 16-row x 128-element tiled layout
+                           // (FMOE_W_INT4_TILED) instead of row-major
   int64_t Kred;            // reduction length (elements)
   int64_t Nout;            // weight rows per expert (GEMM1: 2N, GEMM2: K)
   int64_t N_act;           // GEMM1: N (columns of act)

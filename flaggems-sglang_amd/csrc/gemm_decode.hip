@@ -13,6 +13,14 @@
 // the per-wave partial accumulators are summed through LDS once at the end.
 // GEMM2 may further split the reduction across workgroups (`splits`); the
 // partials land in separate y planes that fmoe_moe_sum adds in fixed order.
+// A workgroup may hold RB such row blocks (RB x 4 waves, RB x 64 rows; the
+// waves of one reduction slice then read the same activation bytes): chosen
+// per format by measurement (decode_row_blocks).
+//
+// int4 weights come row-major ([rows][K/2]: one load instruction touches 16
+// rows x 64 bytes, half cache lines) or tiled (FMOE_W_INT4_TILED: each 16-row
+// x 64-byte block stored contiguously in lane order, so the same instruction
+// reads one contiguous KiB); only the addresses differ, results are identical.
 //
 // Weight formats (one stage = one 128-byte slice of a weight row, int4: 64):
 //   bf16: 16 elements per lane -> two v_mfma_f32_16x16x32_bf16.
@@ -35,15 +43,27 @@
 namespace fmoe {
 namespace decode {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
+constexpr int kThreads = 256;  // one row block: 4 waves
+constexpr int kWaves = 4;      // waves splitting the reduction dim of a row block
+constexpr int kMaxRB = 2;
 constexpr int BM = 16;
 constexpr int BN = 64;
 constexpr int NI = BN / 16;
 
+// Weight loads: streamed once per call.
+__device__ __forceinline__ i32x4_t wload16(const uint8_t* p) {
+  return *reinterpret_cast<const i32x4_t*>(p);
+}
+
 __device__ __forceinline__ i32x8_t gload32(const uint8_t* p) {
   i32x4_t lo = *reinterpret_cast<const i32x4_t*>(p);
   i32x4_t hi = *reinterpret_cast<const i32x4_t*>(p + 16);
+  return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__device__ __forceinline__ i32x8_t wload32(const uint8_t* p) {
+  i32x4_t lo = wload16(p);
+  i32x4_t hi = wload16(p + 16);
   return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -99,25 +119,27 @@ struct TinyLds {
   int ids[kTinySlots];
   int rows[BM];
   int info[4];     // expert, block, rows in the tile, valid
-  int scan[kWaves];
+  int scan[kWaves * kMaxRB];
 };
 
 // Returns false when tile mt does not exist (same decision in every thread).
+// NT = threads of the workgroup.
+template <int NT>
 __device__ bool tiny_route(const GemmParams& p, int mt, TinyLds& L) {
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
   const int E = p.n_experts;
   const int n = static_cast<int>(p.n_tokens * p.top_k);
-  for (int e = tid; e < E; e += kThreads) L.cnt[e] = 0;
+  for (int e = tid; e < E; e += NT) L.cnt[e] = 0;
   if (tid == 0) L.info[3] = 0;
   __syncthreads();
-  for (int f = tid; f < n; f += kThreads) {
+  for (int f = tid; f < n; f += NT) {
     const int id = p.tiny_ids[f];
     L.ids[f] = id;
     if (id >= 0 && id < E) atomicAdd(&L.cnt[id], 1);
   }
   __syncthreads();
   // tiles per expert = ceil(count / 16); thread t owns experts [t*per, t*per+per)
-  const int per = (E + kThreads - 1) / kThreads;
+  const int per = (E + NT - 1) / NT;
   int mine = 0;
   for (int i = 0; i < per; ++i) {
     const int e = tid * per + i;
@@ -153,7 +175,7 @@ __device__ bool tiny_route(const GemmParams& p, int mt, TinyLds& L) {
   // rows: the [blk*16, blk*16+16) occurrences of expert e in flat order
   const int e = L.info[0], lo = L.info[1] * BM;
   int run = 0;
-  for (int c0 = 0; c0 < n; c0 += kThreads) {
+  for (int c0 = 0; c0 < n; c0 += NT) {
     const int f = c0 + tid;
     const bool hit = f < n && L.ids[f] == e;
     const uint64_t m = __ballot(hit);
@@ -165,25 +187,27 @@ __device__ bool tiny_route(const GemmParams& p, int mt, TinyLds& L) {
     for (int w = 0; w < wid; ++w) off += L.scan[w];
     const int pos = off + before;
     if (hit && pos >= lo && pos < lo + BM) L.rows[pos - lo] = f;
-    for (int w = 0; w < kWaves; ++w) run += L.scan[w];
+    for (int w = 0; w < NT / kWave; ++w) run += L.scan[w];
   }
   __syncthreads();
   return true;
 }
 
-template <WType WT, Mode MODE, int PIPE, int ACT, bool TINY>
-__global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
-  __shared__ f32x4_t red[kWaves][NI][kWave];
+template <WType WT, Mode MODE, int PIPE, int ACT, bool TINY, int RB>
+__global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p) {
+  __shared__ f32x4_t red[RB][kWaves][NI][kWave];
   __shared__ TinyLds tiny_lds[1];  // used by the TINY variant only
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
+  const int kw = wid % kWaves;  // reduction-dim slice of this wave
+  const int rb = wid / kWaves;  // row block of this wave
   const int mt = blockIdx.x;
-  const int nt = blockIdx.y;
+  const int nt = blockIdx.y * RB + rb;  // 64-row block index
   const int split = blockIdx.z;
 
   // this tile: expert e and its rows (slot of tile row r = slot_of(r), r < n_rows)
   int e, row_beg = 0, n_rows;
   if constexpr (TINY) {
-    if (!tiny_route(p, mt, tiny_lds[0])) return;
+    if (!tiny_route<kThreads * RB>(p, mt, tiny_lds[0])) return;
     e = tiny_lds[0].info[0];
     n_rows = tiny_lds[0].info[2];
   } else {
@@ -219,6 +243,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
     int64_t r;
     if (MODE == Mode::kGemm1Silu) {
       int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + (lane & 15);
+      if (jj >= p.N_act) jj = p.N_act - 1;  // last row block of an RB > 1 grid
       r = gemm1_row(ACT, p.N_act, jj, j < NI / 2 ? 0 : 1);
     } else {
       r = static_cast<int64_t>(nt) * BN + j * 16 + (lane & 15);
@@ -226,9 +251,16 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
     }
     wrow[j] = r;
   }
+  // Weight row r's stage-kt slice: row-major at r * w_bytes + kt * kWStage;
+  // int4 tiled: 1 KiB blocks of 16 rows x 64 bytes (one quant group), lane
+  // order inside, so the 64 lanes of a load read one block contiguously.
+  const bool tiled = kInt4 && p.b_tiled;
+  const int64_t w_stride = tiled ? 1024 : kWStage;  // bytes between a row's stages
   const uint8_t* w_ptr[NI];
 #pragma unroll
-  for (int j = 0; j < NI; ++j) w_ptr[j] = Be + wrow[j] * w_bytes + lane_off_w;
+  for (int j = 0; j < NI; ++j)
+    w_ptr[j] = tiled ? Be + (wrow[j] >> 4) * 16 * w_bytes + (lane >> 4) * 256 + (wrow[j] & 15) * 16
+                     : Be + wrow[j] * w_bytes + lane_off_w;
 
   // fp8 weight-scale row of each lane's weight rows
   const int ksb = static_cast<int>(p.Kred / 128);
@@ -244,24 +276,24 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
   for (int j = 0; j < NI; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   auto load = [&](int kt, Stage<WT>& S) {
-    const int64_t woff = static_cast<int64_t>(kt) * kWStage;
+    const int64_t woff = static_cast<int64_t>(kt) * w_stride;
     const uint8_t* ap = a_ptr + static_cast<int64_t>(kt) * kElems * 2 + lane_off_a;
     if constexpr (WT == WType::kBf16) {
       S.a = gload32(ap);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = wload32(w_ptr[j] + woff);
     } else if constexpr (WT == WType::kFp8) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = wload32(w_ptr[j] + woff);
 #pragma unroll
       for (int j = 0; j < NI; ++j) S.sb[j] = sb_ptr[j][kt];
     } else if constexpr (kMx) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = wload16(w_ptr[j] + woff);
       // this lane's 32 elements are scale block 4 kt + lane / 16 of its row
       const int64_t nblk = p.Kred / 32;
 #pragma unroll
@@ -271,7 +303,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = wload16(w_ptr[j] + woff);
       // scale and zero of group kt for this lane's column, fetched with the
       // weights so that the stage's loads complete together
       const int64_t gbase = (static_cast<int64_t>(e) * (p.Kred / 128) + kt) * p.Nout;
@@ -405,7 +437,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
   const int k_end = min(nk, k_beg + per_split);
   if constexpr (PIPE == 2) {
     Stage<WT> s0, s1;
-    int kt = k_beg + wid;
+    int kt = k_beg + kw;
     if (kt < k_end) load(kt, s0);
     while (kt < k_end) {
       const int k1 = kt + kWaves;
@@ -418,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
       kt = k2;
     }
   } else {
-    for (int kt = k_beg + wid; kt < k_end; kt += kWaves) {
+    for (int kt = k_beg + kw; kt < k_end; kt += kWaves) {
       Stage<WT> s0;
       load(kt, s0);
       consume(kt, s0);
@@ -427,15 +459,15 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 
   // ---- reduce the 4 waves' partials
 #pragma unroll
-  for (int j = 0; j < NI; ++j) red[wid][j][lane] = acc[j];
+  for (int j = 0; j < NI; ++j) red[rb][kw][j][lane] = acc[j];
   __syncthreads();
-  if (wid != 0) return;
+  if (kw != 0) return;
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
-    f32x4_t v = red[0][j][lane];
+    f32x4_t v = red[rb][0][j][lane];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) {
-      f32x4_t u = red[w][j][lane];
+      f32x4_t u = red[rb][w][j][lane];
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] += u[r];
     }
@@ -454,6 +486,7 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 #pragma unroll
       for (int j = 0; j < NI / 2; ++j) {
         const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + j * 16 + col16;
+        if (col >= p.N_act) continue;
         float gb, ub;
         gemm1_bias<ACT>(p, e, col, gb, ub);
         act[col] = f32_to_bf16(gemm1_act<ACT>(p, acc[j][r], acc[j + NI / 2][r], gb, ub, g));
@@ -475,23 +508,57 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmParams p) {
 
 }  // namespace decode
 
+// Row blocks per workgroup by format and GEMM (build-time overridable for
+// measurements).
+#ifndef FMOE_DECODE_RB_BF16
+#define FMOE_DECODE_RB_BF16 1
+#endif
+#ifndef FMOE_DECODE_RB_FP8
+#define FMOE_DECODE_RB_FP8 2
+#endif
+#ifndef FMOE_DECODE_RB_INT4
+#define FMOE_DECODE_RB_INT4 1
+#endif
+#ifndef FMOE_DECODE_RB_MXFP4
+#define FMOE_DECODE_RB_MXFP4 2
+#endif
+constexpr int decode_row_blocks(WType wt) {
+  return wt == WType::kBf16 ? FMOE_DECODE_RB_BF16
+         : wt == WType::kFp8 ? FMOE_DECODE_RB_FP8
+         : wt == WType::kInt4 ? FMOE_DECODE_RB_INT4
+                              : FMOE_DECODE_RB_MXFP4;
+}
+static_assert(decode_row_blocks(WType::kBf16) >= 1 && decode_row_blocks(WType::kBf16) <= decode::kMaxRB &&
+                  decode_row_blocks(WType::kFp8) >= 1 && decode_row_blocks(WType::kFp8) <= decode::kMaxRB &&
+                  decode_row_blocks(WType::kInt4) >= 1 && decode_row_blocks(WType::kInt4) <= decode::kMaxRB &&
+                  decode_row_blocks(WType::kMxfp4) >= 1 && decode_row_blocks(WType::kMxfp4) <= decode::kMaxRB,
+              "decode row blocks out of range");
+
 int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   GemmParams p = p0;
   const int64_t ncols = mode == Mode::kGemm1Silu ? p.N_act : p.Nout;
-  const int per_tile = mode == Mode::kGemm1Silu ? decode::BN / 2 : decode::BN;
-  p.n_ntiles = static_cast<int>((ncols + per_tile - 1) / per_tile);
+  const int per_block = mode == Mode::kGemm1Silu ? decode::BN / 2 : decode::BN;
+  const int rbk = decode_row_blocks(wt);
+  const int64_t nblocks = (ncols + per_block - 1) / per_block;
+  p.n_ntiles = static_cast<int>((nblocks + rbk - 1) / rbk);  // workgroups along the output rows
   if (p.max_tiles <= 0) return FMOE_OK;
   dim3 g(static_cast<unsigned>(p.max_tiles), static_cast<unsigned>(p.n_ntiles),
          static_cast<unsigned>(mode == Mode::kGemm2 ? p.splits : 1));
-  dim3 b(decode::kThreads);
-#define LAUNCH(WT_, MODE_, ACT_)                                                                \
-  ((p.tiny_ids && WT_ != WType::kInt4 && WT_ != WType::kMxfp4)                              \
-       ? decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, true><<<g, b, 0, s>>>(p) \
-       : decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, false><<<g, b, 0, s>>>(p))
-#define LAUNCH_G1(WT_)                                                 \
-  (p.act == kActSwiglu ? LAUNCH(WT_, Mode::kGemm1Silu, kActSwiglu)     \
-   : p.act == kActGelu ? LAUNCH(WT_, Mode::kGemm1Silu, kActGelu)       \
-                       : LAUNCH(WT_, Mode::kGemm1Silu, kActSilu))
+#define LAUNCH(WT_, MODE_, ACT_)                                                                      \
+  do {                                                                                                \
+    constexpr int RB_ = decode_row_blocks(WT_);                                                       \
+    const dim3 b_(decode::kThreads * RB_);                                                            \
+    if (p.tiny_ids && WT_ != WType::kInt4 && WT_ != WType::kMxfp4)                                    \
+      decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, true, RB_><<<g, b_, 0, s>>>(p); \
+    else                                                                                              \
+      decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, false, RB_><<<g, b_, 0, s>>>(p); \
+  } while (0)
+#define LAUNCH_G1(WT_)                                    \
+  do {                                                    \
+    if (p.act == kActSwiglu) LAUNCH(WT_, Mode::kGemm1Silu, kActSwiglu); \
+    else if (p.act == kActGelu) LAUNCH(WT_, Mode::kGemm1Silu, kActGelu); \
+    else LAUNCH(WT_, Mode::kGemm1Silu, kActSilu);        \
+  } while (0)
   if (mode == Mode::kGemm1Silu) {
     switch (wt) {
       case WType::kBf16: LAUNCH_G1(WType::kBf16); break;

@@ -138,6 +138,23 @@ __global__ __launch_bounds__(kThreads) void zeros_scales_kernel(int fmt, const u
   so[row * N + 2 * p + 1] = sc[row * N + 2 * p + 1];
 }
 
+// FMOE_W_INT4 q [E][R][K/2] -> FMOE_W_INT4_TILED [E][R/16][K/128][1024]: one
+// thread per 16-byte chunk, threads in source order (coalesced reads); chunk
+// g of row 16b + r's 64-byte group slice c lands at 16 (16 g + r) of block
+// (b, c).
+__global__ __launch_bounds__(kThreads) void tile_int4_kernel(const i32x4_t* __restrict__ q,
+                                                             int64_t chunks, int64_t K,
+                                                             i32x4_t* __restrict__ out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (idx >= chunks) return;
+  const int64_t cpr = K / 32;  // 16-byte chunks per row (K/2 bytes)
+  const int64_t row = idx / cpr;  // flattened over experts: e * R + r
+  const int64_t ch = idx % cpr;
+  const int64_t c = ch / 4, g = ch % 4;
+  const int64_t b = row / 16, r = row % 16;
+  out[(b * (K / 128) + c) * 64 + g * 16 + r] = q[idx];
+}
+
 }  // namespace repack
 }  // namespace fmoe
 
@@ -183,4 +200,26 @@ extern "C" int fmoe_repack_int4(int format, const int32_t* qweight, const int32_
       format, reinterpret_cast<const uint32_t*>(qzeros), scales, pairs, N, zeros_out, scales_out,
       bad_zeros);
   return fmoe_host::check_launch("repack_int4 zeros");
+}
+
+extern "C" int fmoe_tile_int4(const uint8_t* q, int64_t E, int64_t R, int64_t K, uint8_t* out,
+                              void* stream) {
+  using namespace fmoe::repack;
+  if (!q || !out) return fmoe_host::fail(FMOE_ERR_INVALID, "tile_int4: null pointer");
+  if (E < 1 || R < 16 || K < 128 || R % 16 || K % 128)
+    return fmoe_host::fail(FMOE_ERR_INVALID,
+                           "tile_int4: need E >= 1, R %% 16 == 0 and K %% 128 == 0 (E=%lld R=%lld K=%lld)",
+                           static_cast<long long>(E), static_cast<long long>(R), static_cast<long long>(K));
+  const int64_t bytes = E * R * (K / 2);
+  const uint8_t* qe = q + bytes;
+  const uint8_t* oe = out + bytes;
+  if (q < oe && out < qe) return fmoe_host::fail(FMOE_ERR_INVALID, "tile_int4: q and out overlap");
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) % 16)
+    return fmoe_host::fail(FMOE_ERR_INVALID, "tile_int4: q and out must be 16-byte aligned");
+  const int64_t chunks = bytes / 16;
+  const int64_t blocks = (chunks + kThreads - 1) / kThreads;
+  if (blocks > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "tile_int4: tensor too large");
+  tile_int4_kernel<<<static_cast<unsigned>(blocks), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      reinterpret_cast<const fmoe::i32x4_t*>(q), chunks, K, reinterpret_cast<fmoe::i32x4_t*>(out));
+  return fmoe_host::check_launch("tile_int4");
 }

@@ -22,7 +22,7 @@ FMOE_ERR_UNSUPPORTED = 2
 FMOE_ERR_WORKSPACE = 3
 FMOE_ERR_HIP = 4
 
-W_BF16, W_FP8, W_INT4, W_MXFP4 = 0, 1, 2, 3
+W_BF16, W_FP8, W_INT4, W_MXFP4, W_INT4_TILED = 0, 1, 2, 3, 4
 ACT_SILU, ACT_GELU, ACT_SWIGLU = 0, 1, 2
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)
@@ -100,6 +100,7 @@ _SIGS = {
     "fmoe_fused_experts": (ctypes.c_int, [ctypes.POINTER(FusedArgs), vp]),
     "fmoe_repack_int4": (ctypes.c_int, [ctypes.c_int, vp, vp, vp, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.c_int64, ctypes.c_int, vp, vp, vp, vp, vp]),
+    "fmoe_tile_int4": (ctypes.c_int, [vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp]),
 }
 
 EXPORTED = tuple(_SIGS)

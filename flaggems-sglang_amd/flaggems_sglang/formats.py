@@ -99,14 +99,15 @@ def repack_gptq_moe(qweight: torch.Tensor, qzeros: torch.Tensor, scales: torch.T
     return q, sc, z
 
 
-def repack_layer_int4(layer: torch.nn.Module, checkpoint_format: str) -> None:
+def repack_layer_int4(layer: torch.nn.Module, checkpoint_format: str, tiled: bool = True) -> None:
     """Convert an int4 MoE layer's checkpoint tensors in place, once.
 
     Reads ``w13_qweight`` / ``w13_qzeros`` / ``w13_scales`` and the ``w2_``
     ones in ``checkpoint_format`` ("awq", "gptq", "gptq_v2"; optional
     ``w13_g_idx`` / ``w2_g_idx``) and replaces them with the W4A16 layout that
-    ``fused_moe_flagos`` passes to the kernels; marks the layer so a second call
-    is a no-op."""
+    ``fused_moe_flagos`` passes to the kernels -- with ``tiled`` (default) the
+    weights in the tiled layout of ``quant.tile_int4``, which the decode
+    kernels stream faster; marks the layer so a second call is a no-op."""
     if getattr(layer, "fmoe_int4_repacked", False):
         return
     for pre in ("w13", "w2"):
@@ -117,6 +118,10 @@ def repack_layer_int4(layer: torch.nn.Module, checkpoint_format: str) -> None:
             q, s, z = repack_awq_moe(qw, qz, sc)
         else:
             q, s, z = repack_gptq_moe(qw, qz, sc, getattr(layer, f"{pre}_g_idx", None), checkpoint_format)
+        if tiled:
+            from .quant import tile_int4
+
+            q = tile_int4(q)
         for name, t in (("qweight", q), ("scales", s), ("qzeros", z)):
             old = getattr(layer, f"{pre}_{name}")
             if isinstance(old, torch.nn.Parameter):

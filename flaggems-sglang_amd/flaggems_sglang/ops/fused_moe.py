@@ -26,7 +26,7 @@ from typing import Optional
 import torch
 
 from .. import _lib
-from .._lib import W_BF16, W_FP8, W_INT4, W_MXFP4, check, lib, ptr, require_cuda, stream_of
+from .._lib import W_BF16, W_FP8, W_INT4, W_INT4_TILED, W_MXFP4, check, lib, ptr, require_cuda, stream_of
 
 logger = logging.getLogger(__name__)
 
@@ -269,7 +269,10 @@ def _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w
         assert w1.dtype == torch.uint8 and w2.dtype == torch.uint8, "int4 weights are packed uint8"
         assert w1_scale is not None and w2_scale is not None and w1_zp is not None and w2_zp is not None, \
             "int4 needs w1_scale, w2_scale, w1_zp and w2_zp"
-        return W_INT4
+        # 4-D weights: the tiled layout of quant.tile_int4 (both or neither)
+        assert w1.dim() == w2.dim() and w1.dim() in (3, 4), \
+            "int4 weights must both be row-major [E, R, C/2] or both tiled [E, R/16, C/128, 1024]"
+        return W_INT4_TILED if w1.dim() == 4 else W_INT4
     assert w1_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="w1_scale")
     assert w2_scale is None, _UNSUPPORTED_FEATURE_MSG.format(name="w2_scale")
     assert block_shape is None, _UNSUPPORTED_FEATURE_MSG.format(name="block_shape")
@@ -289,6 +292,15 @@ def _act_code(activation: str) -> int:
     return _ACTIVATIONS[activation]
 
 
+def _weight_dims(w, wtype):
+    """(experts, rows, reduction length) of a weight tensor in any layout."""
+    if wtype == W_INT4_TILED:
+        assert w.shape[3] == 1024, "tiled int4 weights must be [E, R/16, C/128, 1024]"
+        return w.shape[0], w.shape[1] * 16, w.shape[2] * 128
+    nib = wtype in (W_INT4, W_MXFP4)
+    return w.shape[0], w.shape[1], w.shape[2] * (2 if nib else 1)
+
+
 def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens, top_k,
                 n_experts, topk_indx, gate_indx, gate_scal, offs_raw, offs_pad, tile_map, n_tiles,
                 block_m, apply_router_weight_on_input, scale, combine=True, act=_lib.ACT_SILU,
@@ -298,7 +310,7 @@ def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens,
     fp32 biases (bias path)."""
     L = lib()
     M, K = x.shape
-    N = w2.shape[2] * (2 if wtype in (W_INT4, W_MXFP4) else 1)
+    N = _weight_dims(w2, wtype)[2]
     dev = x.device
     st = stream_of(x)
     r = _lib.Routing(ptr(topk_indx), ptr(gate_indx), ptr(gate_scal), ptr(offs_raw), ptr(offs_pad),
@@ -549,6 +561,9 @@ def fused_experts(
            uint8 (two uint4 per byte, low nibble first), ``w1_scale [E, K/128, 2N]``
            / ``w2_scale [E, N/128, K]`` fp16, ``w1_zp [E, K/128, N]`` /
            ``w2_zp [E, N/128, K/2]`` uint8 (two uint4 zeros per byte);
+           The same weights tiled by ``quant.tile_int4`` (4-D ``[E, R/16,
+           C/128, 1024]``, scales and zeros unchanged) take the decode kernels'
+           contiguous-block loads;
       mxfp4 (``use_mxfp4_w4a16``): OCP MXFP4 ``w1 [E, 2N, K/2]`` / ``w2 [E, K, N/2]``
            uint8 (two e2m1 per byte, low nibble first), ``w1_scale [E, 2N, K/32]`` /
            ``w2_scale [E, K, N/32]`` e8m0 bytes; bf16 activations (the streaming
@@ -570,16 +585,14 @@ def fused_experts(
     require_cuda(hidden_states, w1, w2, topk_weights, topk_ids, w1_scale, w2_scale, w1_zp, w2_zp)
     x = hidden_states.contiguous()
     M, K = x.shape
-    E = w1.shape[0]
+    E, rows1, kin = _weight_dims(w1, wtype)
+    _, rows2, N = _weight_dims(w2, wtype)
     k = topk_ids.shape[1]
-    nib = wtype in (W_INT4, W_MXFP4)
-    N = w2.shape[2] * (2 if nib else 1)
-    kin = w1.shape[2] * (2 if nib else 1)
     if wtype == W_MXFP4:
         assert tuple(w1_scale.shape) == (E, 2 * N, K // 32) and tuple(w2_scale.shape) == (E, K, N // 32), \
             "mxfp4 scales must be [E, 2N, K/32] and [E, K, N/32]"
         w1_scale, w2_scale = w1_scale.view(torch.uint8), w2_scale.view(torch.uint8)
-    assert kin == K and w1.shape[1] == 2 * N and w2.shape[1] == K, "weight shapes do not match"
+    assert kin == K and rows1 == 2 * N and rows2 == K and w2.shape[0] == E, "weight shapes do not match"
     for t in (w1, w2, w1_scale, w2_scale, w1_zp, w2_zp):
         if t is not None:
             assert t.is_contiguous(), "weights and scales must be contiguous"

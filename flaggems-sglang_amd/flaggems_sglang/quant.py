@@ -1,12 +1,15 @@
 """Weight preparation for the quantized fused-MoE paths (load time, not the
-hot path): fp8-e4m3fn 128x128 block quantization and uint4 group
-quantization into the layouts ``fused_experts`` reads.  Plain torch, on
-whatever device the weights live.
+hot path): fp8-e4m3fn 128x128 block quantization, uint4 group and MXFP4
+quantization into the layouts ``fused_experts`` reads (plain torch, on
+whatever device the weights live), and the tiling of int4 weights for the
+decode kernels (``tile_int4``, a HIP kernel).
 """
 
 from __future__ import annotations
 
 import torch
+
+from . import _lib
 
 FP8_MAX = 448.0
 FP8_EPS = 1e-10
@@ -86,3 +89,20 @@ def quantize_mxfp4(w: torch.Tensor, block: int = 32):
     c = c | (torch.signbit(a).to(torch.uint8) << 3)
     c = c.view(E, R, C)
     return (c[..., 0::2] | (c[..., 1::2] << 4)).contiguous(), scale.contiguous()
+
+
+def tile_int4(q: torch.Tensor) -> torch.Tensor:
+    """Row-major int4 weights ``q [E, R, C/2]`` u8 (as ``quantize_int4_group``
+    returns them) -> the tiled layout ``[E, R/16, C/128, 1024]`` that
+    ``fused_experts`` streams with one contiguous 1 KiB read per 16 rows x one
+    128-element group (``fmoe_tile_int4``, on the GPU).  Scales and zeros
+    keep their layout.  Needs R % 16 == 0 and C % 128 == 0."""
+    _lib.require_cuda(q)
+    assert q.dtype == torch.uint8 and q.dim() == 3, "tile_int4 takes packed uint8 [E, R, C/2]"
+    q = q.contiguous()
+    E, R, half = q.shape
+    K = 2 * half
+    out = torch.empty(E, R // 16, K // 128, 1024, dtype=torch.uint8, device=q.device)
+    _lib.check(_lib.lib().fmoe_tile_int4(_lib.ptr(q), E, R, K, _lib.ptr(out), _lib.stream_of(q)),
+               "tile_int4")
+    return out

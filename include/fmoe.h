@@ -50,6 +50,9 @@ enum fmoe_wtype {
                           dim), bf16 activations: w13 [E, 2N, K/2] u8 + scale [E, 2N, K/32] u8,
                           w2 [E, K, N/2] u8 + scale [E, K, N/32] u8; element 2i in the low
                           nibble; w = e2m1(q) * 2^(s - 127) */
+  FMOE_W_INT4_TILED = 4, /* FMOE_W_INT4 with the weight bytes tiled for the decode kernels
+                            (scales and zeros unchanged): w13 [E, 2N/16, K/128, 1024],
+                            w2 [E, K/16, N/128, 1024]; see fmoe_tile_int4 */
 };
 
 /* GEMM1 activations (the fused epilogue of fmoe_gemm1_ex / fmoe_fused_experts). */
@@ -321,6 +324,17 @@ int fmoe_repack_int4(int format, const int32_t* qweight, const int32_t* qzeros,
                      const uint16_t* scales, int64_t E, int64_t K, int64_t N, int group,
                      uint8_t* q_out, uint16_t* scales_out, uint8_t* zeros_out,
                      int32_t* bad_zeros, void* stream);
+
+/* Load-time tiling of FMOE_W_INT4 weights into FMOE_W_INT4_TILED.  No
+ * counterpart in the reference (its W4A16 kernels read the row-major
+ * layout on every call); for callers that prepare weights once, as after
+ * fmoe_repack_int4.  q [E, R, K/2] u8 (row r, element 2i low nibble) ->
+ * out [E, R/16, K/128, 1024]: block (b, c) holds rows 16b..16b+15, bytes
+ * 64c..64c+63 of each (one 128-element quant group), byte 16 (16 g + r) + i
+ * = byte 64c + 16g + i of row 16b + r.  A decode wave's 16-row x 64-byte
+ * weight load is then one contiguous 1 KiB read.  Needs R % 16 == 0 and
+ * K % 128 == 0; q and out must not overlap. */
+int fmoe_tile_int4(const uint8_t* q, int64_t E, int64_t R, int64_t K, uint8_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,6 +21,12 @@ pack / unpack round trips and by dequantization invariance (a checkpoint and
 its repacked form dequantize to identical values), all in
 tests/test_formats.py.
 
+The tiled int4 layout (``fmoe_tile_int4``, FMOE_W_INT4_TILED) has no
+counterpart in the reference or in those libraries; ``tile_int4`` restates
+its definition, and tests/test_int4_tiled.py pins it by known-answer
+positions, the round trip through ``untile_int4``, and bit-identical
+fused-MoE outputs from tiled and row-major weights.
+
 Target layout (the W4A16 kernels, ``fused_moe_oracle.quant_int4``):
 qweight [N, K/2] u8 (element 2i low nibble), scales [K/g, N] fp16, zeros
 [K/g, N/2] u8 (row 2j low nibble).
@@ -141,3 +147,20 @@ def dequant_checkpoint(q_kn, z_gn, s_gn, group: int):
     sk = np.repeat(np.asarray(s_gn, dtype=np.float32), group, axis=-2)
     w = (q_kn.astype(np.float32) - zk) * sk
     return np.ascontiguousarray(np.swapaxes(w, -1, -2))
+
+
+# ------------------------------------------------------------ tiled layout
+def tile_int4(q: np.ndarray) -> np.ndarray:
+    """Row-major ``q [E, R, K/2]`` u8 -> ``[E, R/16, K/128, 1024]``: block
+    (b, c) holds rows 16b..16b+15 x bytes 64c..64c+63; byte 16 (16 g + r) + i
+    of the block = byte 64c + 16g + i of row 16b + r."""
+    E, R, half = q.shape
+    K = 2 * half
+    v = q.reshape(E, R // 16, 16, K // 128, 4, 16)     # e, b, r, c, g, i
+    return np.ascontiguousarray(v.transpose(0, 1, 3, 4, 2, 5)).reshape(E, R // 16, K // 128, 1024)
+
+
+def untile_int4(t: np.ndarray) -> np.ndarray:
+    E, B, C, _ = t.shape
+    v = t.reshape(E, B, C, 4, 16, 16)                   # e, b, c, g, r, i
+    return np.ascontiguousarray(v.transpose(0, 1, 4, 2, 3, 5)).reshape(E, B * 16, C * 64)

@@ -209,7 +209,8 @@ def test_gpu_checkpoint_to_fused_experts_end_to_end(fmt):
 @pytest.mark.gpu
 def test_gpu_flagos_hook_repacks_awq_layer_once():
     """fused_moe_flagos on a layer holding AWQ checkpoint tensors: converted
-    on the first call, reused after, same output as the W4A16-layout layer."""
+    (and tiled) on the first call, reused after, same output as the
+    row-major W4A16-layout layer."""
     from types import SimpleNamespace
 
     from flaggems_sglang import quant as Q
@@ -241,5 +242,8 @@ def test_gpu_flagos_hook_repacks_awq_layer_once():
     ref = fused_moe_flagos(obj, native, disp).hidden_states
     out1 = fused_moe_flagos(obj, awq, disp).hidden_states
     assert awq.fmoe_int4_repacked and awq.w13_qweight.dtype == torch.uint8
+    # repacked into the tiled layout (quant.tile_int4) by default
+    assert awq.w13_qweight.shape == (E, 2 * N // 16, K // 128, 1024)
+    assert awq.w2_qweight.shape == (E, K // 16, N // 128, 1024)
     out2 = fused_moe_flagos(obj, awq, disp).hidden_states
     assert torch.equal(out1, ref) and torch.equal(out2, ref)

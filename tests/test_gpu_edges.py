@@ -17,7 +17,7 @@ from oracle import fused_moe_oracle as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-FORMATS = ["bf16", "fp8", "int4", "mxfp4"]
+FORMATS = ["bf16", "fp8", "int4", "int4t", "mxfp4"]  # int4t: tiled int4 weights
 
 
 def _weights(fmt, d):
@@ -28,9 +28,11 @@ def _weights(fmt, d):
         q1, s1 = Q.quantize_fp8_block(w13)
         q2, s2 = Q.quantize_fp8_block(w2)
         return q1, q2, dict(use_fp8_w8a8=True, w1_scale=s1, w2_scale=s2, block_shape=[128, 128])
-    if fmt == "int4":
+    if fmt in ("int4", "int4t"):
         q1, s1, z1 = Q.quantize_int4_group(w13)
         q2, s2, z2 = Q.quantize_int4_group(w2)
+        if fmt == "int4t":
+            q1, q2 = Q.tile_int4(q1), Q.tile_int4(q2)
         return q1, q2, dict(use_int4_w4a16=True, w1_scale=s1, w2_scale=s2, w1_zp=z1, w2_zp=z2)
     q1, s1 = Q.quantize_mxfp4(w13)
     q2, s2 = Q.quantize_mxfp4(w2)
@@ -43,7 +45,11 @@ def _oracle(fmt, d, q1, q2, kw):
         return O.fused_experts(d["x"], d["w13"], d["w2"], *args)
     if fmt == "fp8":
         return O.fused_experts_fp8(d["x"], q1.cpu(), kw["w1_scale"].cpu(), q2.cpu(), kw["w2_scale"].cpu(), *args)
-    if fmt == "int4":
+    if fmt in ("int4", "int4t"):
+        if fmt == "int4t":
+            from oracle import formats_oracle as FO
+            q1 = torch.from_numpy(FO.untile_int4(q1.cpu().numpy()))
+            q2 = torch.from_numpy(FO.untile_int4(q2.cpu().numpy()))
         return O.fused_experts_w4a16(d["x"], q1.cpu(), kw["w1_scale"].cpu(), kw["w1_zp"].cpu(), q2.cpu(),
                                      kw["w2_scale"].cpu(), kw["w2_zp"].cpu(), *args)
     return O.fused_experts_mxfp4(d["x"], q1.cpu(), kw["w1_scale"].cpu(), q2.cpu(), kw["w2_scale"].cpu(), *args)

@@ -1,0 +1,147 @@
+"""Tiled int4 weights (``quant.tile_int4`` / ``fmoe_tile_int4``, weight type
+FMOE_W_INT4_TILED): the layout the W4A16 decode kernels read with one
+contiguous 1 KiB load per 16 rows x one 128-element quant group.
+
+CPU: the oracle's tile / untile against known-answer positions and its round
+trip; the host check that both weights use the same layout.  GPU: the tiling
+kernel bit-exact against the oracle (and its argument checks), and the fused
+op on tiled weights bit-identical to the same weights row-major (same
+kernels, same reduction order: only the weight addresses change), across
+decode and larger batches, both activations, an expert map, no_combine and
+the stage-level C ABI.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats_oracle as FO
+
+DEV = "cuda"
+
+
+# ----------------------------------------------------------------- CPU
+def test_oracle_tile_known_positions():
+    # every 16-byte chunk of q holds (row, chunk) so its destination names it
+    E, R, K = 2, 48, 384
+    half = K // 2
+    q = np.zeros((E, R, half), dtype=np.uint8)
+    for e in range(E):
+        for r in range(R):
+            for ch in range(half // 16):
+                q[e, r, 16 * ch:16 * ch + 16] = [e, r, ch] + [0xA5] * 13
+    t = FO.tile_int4(q)
+    assert t.shape == (E, R // 16, K // 128, 1024)
+    flat = t.reshape(E, -1)
+    # row 17, chunk 5 = group c 1, lane group g 1; block b 1, r 1:
+    # byte offset ((b * K/128 + c) * 1024) + (16 g + r) * 16
+    off = (1 * (K // 128) + 1) * 1024 + (16 * 1 + 1) * 16
+    assert list(flat[1, off:off + 3]) == [1, 17, 5]
+    # row 0, chunk 0 -> offset 0; row 15, chunk 3 (c 0, g 3) -> (48 + 15) * 16
+    assert list(flat[0, 0:3]) == [0, 0, 0]
+    assert list(flat[0, 63 * 16:63 * 16 + 3]) == [0, 15, 3]
+    # row 47, last chunk (c 2, g 3), block 2
+    off = (2 * 3 + 2) * 1024 + (48 + 15) * 16
+    assert list(flat[1, off:off + 3]) == [1, 47, half // 16 - 1]
+    # each 1 KiB block holds 16 distinct rows x 4 chunks of one group
+    blk = t[0, 1, 2].reshape(64, 16)
+    assert sorted({(int(c[1]), int(c[2])) for c in blk}) == sorted(
+        (16 + r, 4 * 2 + g) for r in range(16) for g in range(4))
+
+
+def test_oracle_tile_round_trip():
+    rng = np.random.default_rng(7)
+    for E, R, K in [(1, 16, 128), (3, 64, 512), (2, 32, 1152)]:
+        q = rng.integers(0, 256, (E, R, K // 2), dtype=np.uint8)
+        t = FO.tile_int4(q)
+        assert np.array_equal(FO.untile_int4(t), q)
+        # a permutation: same byte multiset per expert
+        assert np.array_equal(np.sort(t.reshape(E, -1), axis=1), np.sort(q.reshape(E, -1), axis=1))
+
+
+def test_host_rejects_mixed_layouts():
+    from flaggems_sglang.ops.fused_moe import _wtype_and_check
+    w3 = torch.zeros(2, 256, 64, dtype=torch.uint8)
+    w4 = torch.zeros(2, 16, 1, 1024, dtype=torch.uint8)
+    s = torch.zeros(1)
+    with pytest.raises(AssertionError, match="both be row-major"):
+        _wtype_and_check(False, True, w3, w4, s, s, s, s, None, False)
+    from flaggems_sglang._lib import W_INT4, W_INT4_TILED
+    assert _wtype_and_check(False, True, w4, w4, s, s, s, s, None, False) == W_INT4_TILED
+    assert _wtype_and_check(False, True, w3, w3, s, s, s, s, None, False) == W_INT4
+
+
+# ----------------------------------------------------------------- GPU
+@pytest.mark.gpu
+@pytest.mark.parametrize("E,R,K", [(1, 16, 128), (3, 64, 512), (2, 48, 1152), (8, 256, 4096)])
+def test_tile_kernel_matches_oracle(E, R, K):
+    from flaggems_sglang import quant as Q
+    g = torch.Generator().manual_seed(E * 1000 + R + K)
+    q = torch.randint(0, 256, (E, R, K // 2), dtype=torch.uint8, generator=g)
+    t = Q.tile_int4(q.to(DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(t.cpu().numpy(), FO.tile_int4(q.numpy()))
+
+
+@pytest.mark.gpu
+def test_tile_kernel_argument_checks():
+    from flaggems_sglang import _lib
+    L = _lib.lib()
+    q = torch.zeros(1, 32, 128, dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(q)
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.fmoe_tile_int4(q.data_ptr(), 1, 32, 256, out.data_ptr(), st) == 0
+    assert L.fmoe_tile_int4(q.data_ptr(), 1, 24, 256, out.data_ptr(), st) != 0  # R % 16
+    assert L.fmoe_tile_int4(q.data_ptr(), 1, 32, 192, out.data_ptr(), st) != 0  # K % 128
+    assert L.fmoe_tile_int4(q.data_ptr(), 1, 32, 256, q.data_ptr() + 1024, st) != 0  # overlap
+    assert b"overlap" in L.fmoe_last_error()
+    assert L.fmoe_tile_int4(None, 1, 32, 256, out.data_ptr(), st) != 0
+    torch.cuda.synchronize()
+
+
+def _int4_layer(M, K, N, E, k):
+    from flaggems_sglang import quant as Q
+    from oracle import fused_moe_oracle as O
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    q1, s1, z1 = Q.quantize_int4_group(d["w13"].to(DEV))
+    q2, s2, z2 = Q.quantize_int4_group(d["w2"].to(DEV))
+    kw = dict(use_int4_w4a16=True, w1_scale=s1, w2_scale=s2, w1_zp=z1, w2_zp=z2)
+    return d, q1, q2, Q.tile_int4(q1), Q.tile_int4(q2), kw
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N,E,k", [(1, 512, 384, 8, 2), (5, 256, 256, 4, 2), (16, 1024, 768, 8, 2),
+                                       (64, 512, 384, 16, 4), (300, 256, 512, 8, 2), (1, 128, 128, 1, 1)])
+@pytest.mark.parametrize("activation", ["silu", "gelu"])
+def test_fused_tiled_equals_row_major(M, K, N, E, k, activation):
+    import flaggems_sglang
+    d, q1, q2, t1, t2, kw = _int4_layer(M, K, N, E, k)
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    ref = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, activation=activation, **kw)
+    out = flaggems_sglang.fused_experts(x, t1, t2, tw, ti, activation=activation, **kw)
+    assert torch.equal(out, ref)
+    if M == 16 and activation == "silu":
+        # and against the dequantizing oracle, as the row-major int4 tests do
+        from oracle import fused_moe_oracle as O
+        o = O.fused_experts_w4a16(d["x"], q1.cpu(), kw["w1_scale"].cpu(), kw["w1_zp"].cpu(), q2.cpu(),
+                                  kw["w2_scale"].cpu(), kw["w2_zp"].cpu(), d["topk_weights"], d["topk_ids"])
+        rel = float((out.float().cpu() - o.float()).norm() / o.float().norm())
+        assert rel < 5e-2 / 4
+
+
+@pytest.mark.gpu
+def test_fused_tiled_expert_map_and_no_combine():
+    import flaggems_sglang
+    M, K, N, E, k = 9, 512, 384, 16, 4
+    d, q1, q2, t1, t2, kw = _int4_layer(M, K, N, E, k)
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    emap = torch.arange(E, dtype=torch.int32, device=DEV)
+    emap[3] = -1
+    a = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, expert_map=emap, global_num_experts=E, **kw)
+    b = flaggems_sglang.fused_experts(x, t1, t2, tw, ti, expert_map=emap, global_num_experts=E, **kw)
+    assert torch.equal(a, b)
+    a = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, no_combine=True, **kw)
+    b = flaggems_sglang.fused_experts(x, t1, t2, tw, ti, no_combine=True, **kw)
+    assert torch.equal(a, b)
