@@ -41,6 +41,8 @@ WORKLOADS = {
     "dsv3_fp8_m4096": (4096, 7168, 2048, 256, 8, "fp8", "grouped"),
     "dsv3_fp8_m8192": (8192, 7168, 2048, 256, 8, "fp8", "grouped"),
     "dsv3_fp8_m1": (1, 7168, 2048, 256, 8, "fp8", "grouped"),
+    "dsv3_fp8_m128": (128, 7168, 2048, 256, 8, "fp8", "grouped"),
+    "qwen3_bf16_m64": (64, 2048, 768, 128, 8, "bf16", "softmax_bias"),
     "mixtral_w4a16_m1": (1, 4096, 14336, 8, 2, "int4", "softmax"),
     "mixtral_w4a16_m16": (16, 4096, 14336, 8, 2, "int4", "softmax"),
     # the same int4 weights tiled at load time (quant.tile_int4)
