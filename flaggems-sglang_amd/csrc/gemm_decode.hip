@@ -200,9 +200,25 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
   const int kw = wid % kWaves;  // reduction-dim slice of this wave
   const int rb = wid / kWaves;  // row block of this wave
-  const int mt = blockIdx.x;
-  const int nt = blockIdx.y * RB + rb;  // 64-row block index
-  const int split = blockIdx.z;
+  int mt = blockIdx.x, ntw = blockIdx.y, split = blockIdx.z;
+  if (!TINY && gridDim.y <= 128) {
+    // Only the first n_tiles x gridDim.y x gridDim.z workgroups have work.
+    // Their ids are remapped so each XCD takes a contiguous run of row
+    // blocks of one (tile, split): the tile's activation rows (and shared
+    // scale / zero lines) then meet in one XCD's L2 instead of being
+    // fetched by every XCD.  Measured: 4-5% faster when tiles are short
+    // (<= 128 row workgroups: DSV3, Qwen3 shapes), 4% slower for Mixtral
+    // GEMM1's 448, which keeps the hardware order.
+    const int gy = gridDim.y;
+    const int live = *p.n_tiles * gy * gridDim.z;
+    const int b = blockIdx.x + gridDim.x * (blockIdx.y + gy * blockIdx.z);
+    if (b >= live) return;
+    const int L = xcd_remap(b, live);
+    ntw = L % gy;
+    mt = (L / gy) % *p.n_tiles;
+    split = L / (gy * *p.n_tiles);
+  }
+  const int nt = ntw * RB + rb;  // 64-row block index
 
   // this tile: expert e and its rows (slot of tile row r = slot_of(r), r < n_rows)
   int e, row_beg = 0, n_rows;
@@ -211,7 +227,7 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
     e = tiny_lds[0].info[0];
     n_rows = tiny_lds[0].info[2];
   } else {
-    if (mt >= *p.n_tiles) return;
+    if (mt >= *p.n_tiles) return;  // tile slot beyond this call's tiles
     const int tm = p.tile_map[mt];
     e = tm & 0xffff;
     const int blk = tm >> 16;
