@@ -51,6 +51,8 @@ WORKLOADS = {
     # OCP MXFP4 weights (e2m1 + e8m0 per 32), bf16 activations
     "mixtral_mxfp4_m1": (1, 4096, 14336, 8, 2, "mxfp4", "softmax"),
     "mixtral_mxfp4_m16": (16, 4096, 14336, 8, 2, "mxfp4", "softmax"),
+    "mixtral_mxfp4t_m1": (1, 4096, 14336, 8, 2, "mxfp4t", "softmax"),
+    "mixtral_mxfp4t_m16": (16, 4096, 14336, 8, 2, "mxfp4t", "softmax"),
 }
 
 
@@ -58,7 +60,7 @@ def _wt_codes():
     from flaggems_sglang import _lib
 
     return {"bf16": _lib.W_BF16, "fp8": _lib.W_FP8, "int4": _lib.W_INT4, "int4t": _lib.W_INT4_TILED,
-            "mxfp4": _lib.W_MXFP4}
+            "mxfp4": _lib.W_MXFP4, "mxfp4t": _lib.W_MXFP4_TILED}
 
 
 def _gen_weights(E, R, C, gen, dev, wtype, chunk=8):
@@ -76,7 +78,7 @@ def _gen_weights(E, R, C, gen, dev, wtype, chunk=8):
             outs.append((w,))
         elif wtype == "fp8":
             outs.append(Q.quantize_fp8_block(w))
-        elif wtype == "mxfp4":
+        elif wtype in ("mxfp4", "mxfp4t"):
             outs.append(Q.quantize_mxfp4(w))
         else:
             outs.append(Q.quantize_int4_group(w))
@@ -85,7 +87,10 @@ def _gen_weights(E, R, C, gen, dev, wtype, chunk=8):
         # scales / zeros are [E, G, R]: concatenate along experts as well
         q, sc, z = (torch.cat([o[i] for o in outs]) for i in range(3))
         return (Q.tile_int4(q) if wtype == "int4t" else q), sc, z
-    return tuple(torch.cat([o[i] for o in outs]) for i in range(len(outs[0])))
+    res = tuple(torch.cat([o[i] for o in outs]) for i in range(len(outs[0])))
+    if wtype == "mxfp4t":
+        res = (Q.tile_mxfp4(res[0]),) + res[1:]
+    return res
 
 
 def make_problem(name, seed=0):
@@ -111,7 +116,7 @@ def make_problem(name, seed=0):
         kw = dict(use_fp8_w8a8=True, w1_scale=w13[1], w2_scale=w2[1], block_shape=[128, 128])
     elif wtype in ("int4", "int4t"):
         kw = dict(use_int4_w4a16=True, w1_scale=w13[1], w2_scale=w2[1], w1_zp=w13[2], w2_zp=w2[2])
-    elif wtype == "mxfp4":
+    elif wtype in ("mxfp4", "mxfp4t"):
         kw = dict(use_mxfp4_w4a16=True, w1_scale=w13[1], w2_scale=w2[1])
     return dict(name=name, M=M, K=K, N=N, E=E, k=k, wtype=wtype, x=x, w13=w13[0], w2=w2[0],
                 tw=tw, ti=ti, kw=kw)
@@ -131,7 +136,7 @@ def weight_bytes_touched(p):
         per = 3 * K * N * 2
     elif p["wtype"] == "fp8":
         per = 3 * K * N + 4 * (2 * N // 128) * (K // 128) + 4 * (K // 128) * (N // 128)
-    elif p["wtype"] == "mxfp4":
+    elif p["wtype"] in ("mxfp4", "mxfp4t"):
         per = 3 * K * N // 2 + 3 * K * N // 32
     else:  # int4, row-major or tiled
         per = 3 * K * N // 2 + 2 * (K // 128) * 2 * N + (K // 128) * N + 2 * (N // 128) * K + (N // 128) * K // 2
@@ -351,6 +356,8 @@ def roofline_gemm1(res):
         K, N = p["K"], p["N"]
         if p["wtype"] in ("int4", "int4t"):
             wb = 2 * N * K // 2 + 2 * (K // 128) * 2 * N + (K // 128) * N
+        elif p["wtype"] in ("mxfp4", "mxfp4t"):
+            wb = 2 * N * K // 2 + 2 * N * K // 32
         elif p["wtype"] == "fp8":
             wb = 2 * N * K + 4 * (2 * N // 128) * (K // 128)
         else:
@@ -463,7 +470,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": {"bf16": "bf16", "fp8": "fp8-e4m3 (fp32 acc)", "int4": "int4 w / bf16 a",
-                  "int4t": "int4 w (tiled) / bf16 a", "mxfp4": "mxfp4 w / bf16 a"}[p["wtype"]],
+                  "int4t": "int4 w (tiled) / bf16 a", "mxfp4": "mxfp4 w / bf16 a",
+                  "mxfp4t": "mxfp4 w (tiled) / bf16 a"}[p["wtype"]],
         "data": "synthetic: x~N(0,1), weights~N(0,0.02) random-init, router logits~N(0,1)",
         "config": {"workload": p["name"], "M": p["M"], "K": p["K"], "N": p["N"], "E": p["E"],
                    "top_k": p["k"], "weights": p["wtype"], "global_batch": p["M"],

@@ -25,15 +25,18 @@ size_t al(size_t v) { return (v + 255) & ~size_t(255); }
 
 bool valid_wtype(int wt) {
   return wt == FMOE_W_BF16 || wt == FMOE_W_FP8 || wt == FMOE_W_INT4 || wt == FMOE_W_MXFP4 ||
-         wt == FMOE_W_INT4_TILED;
+         wt == FMOE_W_INT4_TILED || wt == FMOE_W_MXFP4_TILED;
 }
 // weight formats that only the streaming (decode) kernels read
 bool is_int4(int wt) { return wt == FMOE_W_INT4 || wt == FMOE_W_INT4_TILED; }
-bool decode_only(int wt) { return is_int4(wt) || wt == FMOE_W_MXFP4; }
+bool is_mx(int wt) { return wt == FMOE_W_MXFP4 || wt == FMOE_W_MXFP4_TILED; }
+bool decode_only(int wt) { return is_int4(wt) || is_mx(wt); }
+// 4-bit weights in the tiled layout of fmoe_tile_int4
+bool is_tiled(int wt) { return wt == FMOE_W_INT4_TILED || wt == FMOE_W_MXFP4_TILED; }
 
 WType to_wt(int wt) {
   return wt == FMOE_W_FP8 ? WType::kFp8
-                          : (is_int4(wt) ? WType::kInt4 : (wt == FMOE_W_MXFP4 ? WType::kMxfp4 : WType::kBf16));
+                          : (is_int4(wt) ? WType::kInt4 : (is_mx(wt) ? WType::kMxfp4 : WType::kBf16));
 }
 
 int check_routing(const fmoe_routing* r, const char* who) {
@@ -185,7 +188,7 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
     return fail(FMOE_ERR_INVALID, "gemm1: fp8 decode takes bf16 x (quantized in-kernel); x_scale must be null");
   if (is_int4(wtype) && (!w13_scale || !w13_zero))
     return fail(FMOE_ERR_INVALID, "gemm1: int4 needs w13_scale and w13_zero");
-  if (wtype == FMOE_W_MXFP4 && !w13_scale)
+  if (is_mx(wtype) && !w13_scale)
     return fail(FMOE_ERR_INVALID, "gemm1: mxfp4 needs w13_scale (e8m0 block scales)");
   if (decode_only(wtype) && !is_decode(r))
     return fail(FMOE_ERR_UNSUPPORTED, "gemm1: int4 / mxfp4 weights need block_m=16 routing");
@@ -199,7 +202,7 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
   p.b_gscale = static_cast<const uint16_t*>(w13_scale);
   p.b_zero = static_cast<const uint8_t*>(w13_zero);
   p.b_mxscale = static_cast<const uint8_t*>(w13_scale);
-  p.b_tiled = wtype == FMOE_W_INT4_TILED;
+  p.b_tiled = is_tiled(wtype);
   p.Kred = K;
   p.Nout = 2 * N;
   p.N_act = N;
@@ -255,7 +258,7 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
     return fail(FMOE_ERR_INVALID, "gemm2: fp8 decode takes bf16 act (quantized in-kernel); act_scale must be null");
   if (is_int4(wtype) && (!w2_scale || !w2_zero))
     return fail(FMOE_ERR_INVALID, "gemm2: int4 needs w2_scale and w2_zero");
-  if (wtype == FMOE_W_MXFP4 && !w2_scale)
+  if (is_mx(wtype) && !w2_scale)
     return fail(FMOE_ERR_INVALID, "gemm2: mxfp4 needs w2_scale (e8m0 block scales)");
   if (decode_only(wtype) && !is_decode(r))
     return fail(FMOE_ERR_UNSUPPORTED, "gemm2: int4 / mxfp4 weights need block_m=16 routing");
@@ -271,7 +274,7 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
   p.b_gscale = static_cast<const uint16_t*>(w2_scale);
   p.b_zero = static_cast<const uint8_t*>(w2_zero);
   p.b_mxscale = static_cast<const uint8_t*>(w2_scale);
-  p.b_tiled = wtype == FMOE_W_INT4_TILED;
+  p.b_tiled = is_tiled(wtype);
   p.Kred = N;
   p.Nout = K;
   p.N_act = N;
@@ -393,7 +396,7 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g1.b_gscale = static_cast<const uint16_t*>(a->w13_scale);
   g1.b_zero = static_cast<const uint8_t*>(a->w13_zero);
   g1.b_mxscale = static_cast<const uint8_t*>(a->w13_scale);
-  g1.b_tiled = a->wtype == FMOE_W_INT4_TILED;
+  g1.b_tiled = is_tiled(a->wtype);
   g1.Kred = a->K;
   g1.Nout = 2 * a->N;
   g1.N_act = a->N;
@@ -408,7 +411,7 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g2.b_gscale = static_cast<const uint16_t*>(a->w2_scale);
   g2.b_zero = static_cast<const uint8_t*>(a->w2_zero);
   g2.b_mxscale = static_cast<const uint8_t*>(a->w2_scale);
-  g2.b_tiled = a->wtype == FMOE_W_INT4_TILED;
+  g2.b_tiled = is_tiled(a->wtype);
   g2.Kred = a->N;
   g2.Nout = a->K;
   g2.N_act = a->N;

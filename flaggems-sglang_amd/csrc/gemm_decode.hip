@@ -17,10 +17,11 @@
 // waves of one reduction slice then read the same activation bytes): chosen
 // per format by measurement (decode_row_blocks).
 //
-// int4 weights come row-major ([rows][K/2]: one load instruction touches 16
-// rows x 64 bytes, half cache lines) or tiled (FMOE_W_INT4_TILED: each 16-row
-// x 64-byte block stored contiguously in lane order, so the same instruction
-// reads one contiguous KiB); only the addresses differ, results are identical.
+// 4-bit weights (int4, MXFP4) come row-major ([rows][K/2]: one load
+// instruction touches 16 rows x 64 bytes, half cache lines) or tiled
+// (FMOE_W_INT4_TILED / FMOE_W_MXFP4_TILED: each 16-row x 64-byte block stored
+// contiguously in lane order, so the same instruction reads one contiguous
+// KiB); only the addresses differ, results are identical.
 //
 // Weight formats (one stage = one 128-byte slice of a weight row, int4: 64):
 //   bf16: 16 elements per lane -> two v_mfma_f32_16x16x32_bf16.
@@ -268,9 +269,9 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
     wrow[j] = r;
   }
   // Weight row r's stage-kt slice: row-major at r * w_bytes + kt * kWStage;
-  // int4 tiled: 1 KiB blocks of 16 rows x 64 bytes (one quant group), lane
+  // 4-bit tiled: 1 KiB blocks of 16 rows x 64 bytes (128 elements), lane
   // order inside, so the 64 lanes of a load read one block contiguously.
-  const bool tiled = kInt4 && p.b_tiled;
+  const bool tiled = kNib && p.b_tiled;
   const int64_t w_stride = tiled ? 1024 : kWStage;  // bytes between a row's stages
   const uint8_t* w_ptr[NI];
 #pragma unroll

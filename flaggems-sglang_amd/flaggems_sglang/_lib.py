@@ -22,7 +22,7 @@ FMOE_ERR_UNSUPPORTED = 2
 FMOE_ERR_WORKSPACE = 3
 FMOE_ERR_HIP = 4
 
-W_BF16, W_FP8, W_INT4, W_MXFP4, W_INT4_TILED = 0, 1, 2, 3, 4
+W_BF16, W_FP8, W_INT4, W_MXFP4, W_INT4_TILED, W_MXFP4_TILED = 0, 1, 2, 3, 4, 5
 ACT_SILU, ACT_GELU, ACT_SWIGLU = 0, 1, 2
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)

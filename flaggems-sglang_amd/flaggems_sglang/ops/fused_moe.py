@@ -26,7 +26,8 @@ from typing import Optional
 import torch
 
 from .. import _lib
-from .._lib import W_BF16, W_FP8, W_INT4, W_INT4_TILED, W_MXFP4, check, lib, ptr, require_cuda, stream_of
+from .._lib import (W_BF16, W_FP8, W_INT4, W_INT4_TILED, W_MXFP4, W_MXFP4_TILED, check, lib, ptr,
+                    require_cuda, stream_of)
 
 logger = logging.getLogger(__name__)
 
@@ -255,7 +256,10 @@ def _wtype_and_check(use_fp8_w8a8, use_int4_w4a16, w1, w2, w1_scale, w2_scale, w
         assert w1_scale.dtype in (torch.uint8, torch.float8_e8m0fnu) and \
             w2_scale.dtype in (torch.uint8, torch.float8_e8m0fnu), "mxfp4 scales are e8m0 bytes"
         assert w1_zp is None and w2_zp is None, _UNSUPPORTED_FEATURE_MSG.format(name="mxfp4 zero points")
-        return W_MXFP4
+        # 4-D weights: tiled by quant.tile_mxfp4 (both or neither)
+        assert w1.dim() == w2.dim() and w1.dim() in (3, 4), \
+            "mxfp4 weights must both be row-major [E, R, C/2] or both tiled [E, R/16, C/128, 1024]"
+        return W_MXFP4_TILED if w1.dim() == 4 else W_MXFP4
     if use_fp8_w8a8:
         assert block_shape is not None and list(block_shape) == [128, 128], \
             _UNSUPPORTED_FEATURE_MSG.format(name=f"block_shape={block_shape}")
@@ -294,8 +298,8 @@ def _act_code(activation: str) -> int:
 
 def _weight_dims(w, wtype):
     """(experts, rows, reduction length) of a weight tensor in any layout."""
-    if wtype == W_INT4_TILED:
-        assert w.shape[3] == 1024, "tiled int4 weights must be [E, R/16, C/128, 1024]"
+    if wtype in (W_INT4_TILED, W_MXFP4_TILED):
+        assert w.shape[3] == 1024, "tiled 4-bit weights must be [E, R/16, C/128, 1024]"
         return w.shape[0], w.shape[1] * 16, w.shape[2] * 128
     nib = wtype in (W_INT4, W_MXFP4)
     return w.shape[0], w.shape[1], w.shape[2] * (2 if nib else 1)
@@ -588,7 +592,7 @@ def fused_experts(
     E, rows1, kin = _weight_dims(w1, wtype)
     _, rows2, N = _weight_dims(w2, wtype)
     k = topk_ids.shape[1]
-    if wtype == W_MXFP4:
+    if wtype in (W_MXFP4, W_MXFP4_TILED):
         assert tuple(w1_scale.shape) == (E, 2 * N, K // 32) and tuple(w2_scale.shape) == (E, K, N // 32), \
             "mxfp4 scales must be [E, 2N, K/32] and [E, K, N/32]"
         w1_scale, w2_scale = w1_scale.view(torch.uint8), w2_scale.view(torch.uint8)

@@ -106,3 +106,10 @@ def tile_int4(q: torch.Tensor) -> torch.Tensor:
     _lib.check(_lib.lib().fmoe_tile_int4(_lib.ptr(q), E, R, K, _lib.ptr(out), _lib.stream_of(q)),
                "tile_int4")
     return out
+
+
+def tile_mxfp4(q: torch.Tensor) -> torch.Tensor:
+    """MXFP4 weight bytes ``q [E, R, C/2]`` (as ``quantize_mxfp4`` returns them)
+    -> the same tiled layout as ``tile_int4`` (both pack two 4-bit elements per
+    byte along C; the e8m0 scales keep their layout)."""
+    return tile_int4(q)

@@ -53,6 +53,8 @@ enum fmoe_wtype {
   FMOE_W_INT4_TILED = 4, /* FMOE_W_INT4 with the weight bytes tiled for the decode kernels
                             (scales and zeros unchanged): w13 [E, 2N/16, K/128, 1024],
                             w2 [E, K/16, N/128, 1024]; see fmoe_tile_int4 */
+  FMOE_W_MXFP4_TILED = 5, /* FMOE_W_MXFP4 with the weight bytes tiled the same way
+                             (fmoe_tile_int4; e8m0 scales unchanged) */
 };
 
 /* GEMM1 activations (the fused epilogue of fmoe_gemm1_ex / fmoe_fused_experts). */
@@ -325,7 +327,8 @@ int fmoe_repack_int4(int format, const int32_t* qweight, const int32_t* qzeros,
                      uint8_t* q_out, uint16_t* scales_out, uint8_t* zeros_out,
                      int32_t* bad_zeros, void* stream);
 
-/* Load-time tiling of FMOE_W_INT4 weights into FMOE_W_INT4_TILED.  No
+/* Load-time tiling of FMOE_W_INT4 weights into FMOE_W_INT4_TILED (and of
+ * FMOE_W_MXFP4 weight bytes, packed the same way, into FMOE_W_MXFP4_TILED).  No
  * counterpart in the reference (its W4A16 kernels read the row-major
  * layout on every call); for callers that prepare weights once, as after
  * fmoe_repack_int4.  q [E, R, K/2] u8 (row r, element 2i low nibble) ->

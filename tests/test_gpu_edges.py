@@ -17,7 +17,7 @@ from oracle import fused_moe_oracle as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-FORMATS = ["bf16", "fp8", "int4", "int4t", "mxfp4"]  # int4t: tiled int4 weights
+FORMATS = ["bf16", "fp8", "int4", "int4t", "mxfp4", "mxfp4t"]  # ...t: tiled 4-bit weights
 
 
 def _weights(fmt, d):
@@ -36,6 +36,8 @@ def _weights(fmt, d):
         return q1, q2, dict(use_int4_w4a16=True, w1_scale=s1, w2_scale=s2, w1_zp=z1, w2_zp=z2)
     q1, s1 = Q.quantize_mxfp4(w13)
     q2, s2 = Q.quantize_mxfp4(w2)
+    if fmt == "mxfp4t":
+        q1, q2 = Q.tile_mxfp4(q1), Q.tile_mxfp4(q2)
     return q1, q2, dict(use_mxfp4_w4a16=True, w1_scale=s1, w2_scale=s2)
 
 
@@ -52,6 +54,10 @@ def _oracle(fmt, d, q1, q2, kw):
             q2 = torch.from_numpy(FO.untile_int4(q2.cpu().numpy()))
         return O.fused_experts_w4a16(d["x"], q1.cpu(), kw["w1_scale"].cpu(), kw["w1_zp"].cpu(), q2.cpu(),
                                      kw["w2_scale"].cpu(), kw["w2_zp"].cpu(), *args)
+    if fmt == "mxfp4t":
+        from oracle import formats_oracle as FO
+        q1 = torch.from_numpy(FO.untile_int4(q1.cpu().numpy()))
+        q2 = torch.from_numpy(FO.untile_int4(q2.cpu().numpy()))
     return O.fused_experts_mxfp4(d["x"], q1.cpu(), kw["w1_scale"].cpu(), q2.cpu(), kw["w2_scale"].cpu(), *args)
 
 
@@ -93,7 +99,7 @@ def _staged_fp8(d, q1, q2, kw):
 @pytest.mark.parametrize("case", ["no_tokens", "one_expert_top1", "min_dims", "all_to_one_expert",
                                   "topk_equals_E", "zero_rows"])
 def test_edge_shapes(fmt, case):
-    tol = 2e-2 if fmt in ("bf16", "mxfp4") else 5e-2
+    tol = 2e-2 if fmt in ("bf16", "mxfp4", "mxfp4t") else 5e-2
     if case == "no_tokens":
         d = O.make_inputs(1, 256, 256, 4, 2, wscale=0.05)
         q1, q2, kw = _weights(fmt, d)

@@ -1,6 +1,7 @@
-"""Tiled int4 weights (``quant.tile_int4`` / ``fmoe_tile_int4``, weight type
-FMOE_W_INT4_TILED): the layout the W4A16 decode kernels read with one
-contiguous 1 KiB load per 16 rows x one 128-element quant group.
+"""Tiled 4-bit weights (``quant.tile_int4`` / ``tile_mxfp4`` /
+``fmoe_tile_int4``, weight types FMOE_W_INT4_TILED and FMOE_W_MXFP4_TILED):
+the layout the decode kernels read with one contiguous 1 KiB load per 16 rows
+x one 128-element quant group.
 
 CPU: the oracle's tile / untile against known-answer positions and its round
 trip; the host check that both weights use the same layout.  GPU: the tiling
@@ -145,3 +146,19 @@ def test_fused_tiled_expert_map_and_no_combine():
     a = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, no_combine=True, **kw)
     b = flaggems_sglang.fused_experts(x, t1, t2, tw, ti, no_combine=True, **kw)
     assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N,E,k", [(1, 512, 384, 8, 2), (16, 1024, 768, 8, 2), (300, 256, 512, 8, 2)])
+def test_fused_mxfp4_tiled_equals_row_major(M, K, N, E, k):
+    import flaggems_sglang
+    from flaggems_sglang import quant as Q
+    from oracle import fused_moe_oracle as O
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    q1, s1 = Q.quantize_mxfp4(d["w13"].to(DEV))
+    q2, s2 = Q.quantize_mxfp4(d["w2"].to(DEV))
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    kw = dict(use_mxfp4_w4a16=True, w1_scale=s1, w2_scale=s2)
+    ref = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, **kw)
+    out = flaggems_sglang.fused_experts(x, Q.tile_mxfp4(q1), Q.tile_mxfp4(q2), tw, ti, **kw)
+    assert torch.equal(out, ref)
