@@ -202,22 +202,29 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
   const int kw = wid % kWaves;  // reduction-dim slice of this wave
   const int rb = wid / kWaves;  // row block of this wave
   int mt = blockIdx.x, ntw = blockIdx.y, split = blockIdx.z;
-  if (!TINY && gridDim.y <= 128) {
-    // Only the first n_tiles x gridDim.y x gridDim.z workgroups have work.
-    // Their ids are remapped so each XCD takes a contiguous run of row
-    // blocks of one (tile, split): the tile's activation rows (and shared
-    // scale / zero lines) then meet in one XCD's L2 instead of being
-    // fetched by every XCD.  Measured: 4-5% faster when tiles are short
-    // (<= 128 row workgroups: DSV3, Qwen3 shapes), 4% slower for Mixtral
-    // GEMM1's 448, which keeps the hardware order.
+  if constexpr (!TINY) {
+    // Only the first n_tiles x gridDim.y x gridDim.z workgroups have work;
+    // their ids are remapped so each XCD takes a contiguous run of the
+    // logical order, in which neighbours share data that then meets in one
+    // XCD's L2 instead of being fetched by every XCD:
+    //  * short tiles (<= 128 row workgroups: DSV3, Qwen3 shapes): row blocks
+    //    fastest, so a tile's activation rows are read by one or two XCDs;
+    //  * long tiles (Mixtral): tiles fastest, so the tiles of one expert at
+    //    the same row block (the same weight bytes) run side by side.
     const int gy = gridDim.y;
-    const int live = *p.n_tiles * gy * gridDim.z;
+    const int ntl = *p.n_tiles;
+    const int live = ntl * gy * gridDim.z;
     const int b = blockIdx.x + gridDim.x * (blockIdx.y + gy * blockIdx.z);
     if (b >= live) return;
     const int L = xcd_remap(b, live);
-    ntw = L % gy;
-    mt = (L / gy) % *p.n_tiles;
-    split = L / (gy * *p.n_tiles);
+    split = L / (gy * ntl);
+    if (gy <= 128) {
+      ntw = L % gy;
+      mt = (L / gy) % ntl;
+    } else {
+      mt = L % ntl;
+      ntw = (L / ntl) % gy;
+    }
   }
   const int nt = ntw * RB + rb;  // 64-row block index
 
@@ -537,7 +544,7 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
 #define FMOE_DECODE_RB_INT4 1
 #endif
 #ifndef FMOE_DECODE_RB_MXFP4
-#define FMOE_DECODE_RB_MXFP4 2
+#define FMOE_DECODE_RB_MXFP4 1
 #endif
 constexpr int decode_row_blocks(WType wt) {
   return wt == WType::kBf16 ? FMOE_DECODE_RB_BF16
