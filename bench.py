@@ -13,7 +13,9 @@ Also on the same line:
                 the host cores) on a bounded token sample of the same workload;
   secondary     north-star points: DeepSeek-V3-shape fp8 W8A8 at M=4096
                 (prefill, % fp8 MFMA peak and % of min(peak, AI*BW)) and
-                Mixtral-shape W4A16 decode at M in {1, 16} (% HBM peak).
+                Mixtral-shape W4A16 decode at M in {1, 4, 16, 64} (tiled int4
+                weights; M=1 / 16 also row-major), % HBM peak; plus DSV3 at
+                M=1 / 128 and Qwen3 at M=64 / 8192 (the other BASELINE configs).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -440,8 +442,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="mixtral_bf16_m4096", choices=sorted(WORKLOADS))
-    ap.add_argument("--secondary", default="dsv3_fp8_m4096,mixtral_w4a16t_m1,mixtral_w4a16t_m16,"
-                                           "mixtral_w4a16_m1,mixtral_w4a16_m16",
+    ap.add_argument("--secondary", default="dsv3_fp8_m4096,mixtral_w4a16t_m1,mixtral_w4a16t_m4,"
+                                           "mixtral_w4a16t_m16,mixtral_w4a16t_m64,mixtral_w4a16_m1,"
+                                           "mixtral_w4a16_m16,dsv3_fp8_m1,dsv3_fp8_m128,qwen3_bf16_m64,"
+                                           "qwen3_bf16_m8192",
                     help="comma list of extra workloads reported in 'secondary' ('' for none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calib", action="store_true",
