@@ -6,10 +6,11 @@
 // its waves by interleaved stages (wave w takes stages w, w+4, ...), so at any
 // moment the four waves read adjacent pieces of the same 64 rows; lane group
 // g = lane/16 reads its part of row lane%16 of each 16-row block.  The fp8
-// GEMM1 variant keeps two stages of loads in flight per wave (its in-register
-// activation quantization is long enough to hide a second stage behind); the
-// others issue one stage at a time, which keeps VGPR use and therefore
-// occupancy higher -- measured faster for bf16 and int4.  No LDS staging;
+// GEMM1 variant with in-workgroup routing (tiny batches) keeps two stages of
+// loads in flight per wave (its in-register activation quantization is long
+// enough to hide a second stage behind); every other variant issues one
+// stage at a time, which keeps VGPR use and therefore occupancy higher --
+// measured faster (see pipe_depth).  No LDS staging;
 // the per-wave partial accumulators are summed through LDS once at the end.
 // GEMM2 may further split the reduction across workgroups (`splits`); the
 // partials land in separate y planes that fmoe_moe_sum adds in fixed order.
@@ -102,8 +103,11 @@ struct Stage<WType::kMxfp4> {
 };
 
 // Stages in flight per wave (see the file comment).
-constexpr int pipe_depth(WType wt, Mode mode) {
-  return wt == WType::kFp8 && mode == Mode::kGemm1Silu ? 2 : 1;
+// (fp8 GEMM1 with in-workgroup routing: two, measured faster at M = 1; with
+// the align launch, e.g. DSV3 M = 128, one stage and twice the occupancy is
+// 7% faster.)
+constexpr int pipe_depth(WType wt, Mode mode, bool tiny) {
+  return wt == WType::kFp8 && mode == Mode::kGemm1Silu && tiny ? 2 : 1;
 }
 
 // Tiny batches (tiles of <= 16 slots, at most kTinySlots slots): the routing
@@ -573,9 +577,9 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
     constexpr int RB_ = decode_row_blocks(WT_);                                                       \
     const dim3 b_(decode::kThreads * RB_);                                                            \
     if (p.tiny_ids && WT_ != WType::kInt4 && WT_ != WType::kMxfp4)                                    \
-      decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, true, RB_><<<g, b_, 0, s>>>(p); \
+      decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_, true), ACT_, true, RB_><<<g, b_, 0, s>>>(p); \
     else                                                                                              \
-      decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_), ACT_, false, RB_><<<g, b_, 0, s>>>(p); \
+      decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_, false), ACT_, false, RB_><<<g, b_, 0, s>>>(p); \
   } while (0)
 #define LAUNCH_G1(WT_)                                    \
   do {                                                    \
