@@ -6,11 +6,12 @@
 // its waves by interleaved stages (wave w takes stages w, w+4, ...), so at any
 // moment the four waves read adjacent pieces of the same 64 rows; lane group
 // g = lane/16 reads its part of row lane%16 of each 16-row block.  The fp8
-// GEMM1 variant with in-workgroup routing (tiny batches) keeps two stages of
-// loads in flight per wave (its in-register activation quantization is long
-// enough to hide a second stage behind); every other variant issues one
-// stage at a time, which keeps VGPR use and therefore occupancy higher --
-// measured faster (see pipe_depth).  No LDS staging;
+// GEMM1 variant with in-workgroup routing (tiny batches) and the MXFP4
+// variants keep two stages of loads in flight per wave (their in-register
+// activation quantization / e2m1 conversion is long enough to hide a second
+// stage behind); every other variant issues one stage at a time, which keeps
+// VGPR use and therefore occupancy higher -- measured faster (see
+// pipe_depth).  No LDS staging;
 // the per-wave partial accumulators are summed through LDS once at the end.
 // GEMM2 may further split the reduction across workgroups (`splits`); the
 // partials land in separate y planes that fmoe_moe_sum adds in fixed order.
@@ -105,9 +106,10 @@ struct Stage<WType::kMxfp4> {
 // Stages in flight per wave (see the file comment).
 // (fp8 GEMM1 with in-workgroup routing: two, measured faster at M = 1; with
 // the align launch, e.g. DSV3 M = 128, one stage and twice the occupancy is
-// 7% faster.)
+// 7% faster.  MXFP4: two, 3-5% faster at M = 16 (its e2m1 conversions hide
+// the second stage), even at M = 1.  bf16 / int4: one.)
 constexpr int pipe_depth(WType wt, Mode mode, bool tiny) {
-  return wt == WType::kFp8 && mode == Mode::kGemm1Silu && tiny ? 2 : 1;
+  return (wt == WType::kFp8 && mode == Mode::kGemm1Silu && tiny) || wt == WType::kMxfp4 ? 2 : 1;
 }
 
 // Tiny batches (tiles of <= 16 slots, at most kTinySlots slots): the routing
