@@ -52,6 +52,8 @@ WORKLOADS = {
     "mixtral_w4a16t_m16": (16, 4096, 14336, 8, 2, "int4t", "softmax"),
     "mixtral_w4a16t_m4": (4, 4096, 14336, 8, 2, "int4t", "softmax"),
     "mixtral_w4a16t_m64": (64, 4096, 14336, 8, 2, "int4t", "softmax"),
+    "mixtral_w4a16t_m256": (256, 4096, 14336, 8, 2, "int4t", "softmax"),
+    "mixtral_w4a16t_m4096": (4096, 4096, 14336, 8, 2, "int4t", "softmax"),
     # OCP MXFP4 weights (e2m1 + e8m0 per 32), bf16 activations
     "mixtral_mxfp4_m1": (1, 4096, 14336, 8, 2, "mxfp4", "softmax"),
     "mixtral_mxfp4_m16": (16, 4096, 14336, 8, 2, "mxfp4", "softmax"),

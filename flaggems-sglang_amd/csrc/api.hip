@@ -4,6 +4,8 @@
 namespace fmoe {
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s);
 int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
+int dequant_4bit(int wtype, const void* q, const void* scale, const void* zeros, int64_t E,
+                 int64_t R, int64_t K, uint16_t* out, hipStream_t s);
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s);
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
@@ -427,8 +429,48 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
 
 }  // namespace
 
+// Large batches of 4-bit weights: the decode kernels re-read an expert's
+// weights for every 16-slot tile, so once experts average kDequantMinSlots
+// slots the weights are dequantized once to bf16 (in the workspace) and the
+// bf16 prefill kernels run on them.  Measured on the Mixtral shape (tiled
+// int4, decode kernels vs dequantize + bf16 prefill): M=512 (128 slots per
+// expert) 1.16 vs 1.66 ms, M=1024 (256) 2.20 vs 2.13 ms, M=4096 8.4 vs 3.8 ms;
+// MXFP4 M=1024 2.81 vs 2.14 ms.
+constexpr int64_t kDequantMinSlots = 256;
+
+bool dequant_prefill(const fmoe_fused_args* a) {
+  if (!decode_only(a->wtype) || a->path == 2) return false;
+  return a->path == 1 || a->M * a->top_k >= kDequantMinSlots * a->E;
+}
+
+// bytes of the bf16 copies of w13 and w2
+size_t dequant_bytes(const fmoe_fused_args* a) {
+  return al(2 * static_cast<size_t>(a->E) * 2 * a->N * a->K) + al(2 * static_cast<size_t>(a->E) * a->K * a->N);
+}
+
+// The same call on bf16 copies of the weights placed at the workspace start.
+fmoe_fused_args bf16_args(const fmoe_fused_args* a, void* ws) {
+  fmoe_fused_args b = *a;
+  b.wtype = FMOE_W_BF16;
+  b.w13_scale = b.w2_scale = nullptr;
+  b.w13_zero = b.w2_zero = nullptr;
+  b.path = 1;
+  b.w13 = b.w2 = nullptr;  // size queries only
+  if (ws) {
+    b.w13 = ws;
+    b.w2 = static_cast<char*>(ws) + al(2 * static_cast<size_t>(a->E) * 2 * a->N * a->K);
+    b.workspace = static_cast<char*>(ws) + dequant_bytes(a);
+    b.workspace_bytes = a->workspace_bytes - dequant_bytes(a);
+  }
+  return b;
+}
+
 extern "C" size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a) {
   if (check_fused(a) != FMOE_OK) return 0;
+  if (dequant_prefill(a)) {
+    const fmoe_fused_args b = bf16_args(a, nullptr);
+    return dequant_bytes(a) + layout(&b).total;
+  }
   return layout(a).total;
 }
 
@@ -437,6 +479,20 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   if (a->M == 0) return FMOE_OK;
   if (!a->x || !a->w13 || !a->w2 || !a->topk_ids || !a->topk_weights || !a->out)
     return fail(FMOE_ERR_INVALID, "fused_experts: null pointer");
+  if (dequant_prefill(a)) {
+    const size_t need = fmoe_fused_experts_workspace_bytes(a);
+    if (!a->workspace || a->workspace_bytes < need)
+      return fail(FMOE_ERR_WORKSPACE, "fused_experts: workspace %zu < %zu bytes", a->workspace_bytes, need);
+    const fmoe_fused_args b = bf16_args(a, a->workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int st = dequant_4bit(a->wtype, a->w13, a->w13_scale, a->w13_zero, a->E, 2 * a->N, a->K,
+                              static_cast<uint16_t*>(const_cast<void*>(b.w13)), s))
+      return st;
+    if (int st = dequant_4bit(a->wtype, a->w2, a->w2_scale, a->w2_zero, a->E, a->K, a->N,
+                              static_cast<uint16_t*>(const_cast<void*>(b.w2)), s))
+      return st;
+    return fmoe_fused_experts(&b, stream);
+  }
   const FusedLayout L = layout(a);
   if (!a->workspace || a->workspace_bytes < L.total)
     return fail(FMOE_ERR_WORKSPACE, "fused_experts: workspace %zu < %zu bytes", a->workspace_bytes,

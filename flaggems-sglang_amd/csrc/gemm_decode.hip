@@ -53,20 +53,9 @@ constexpr int BM = 16;
 constexpr int BN = 64;
 constexpr int NI = BN / 16;
 
-// Weight loads: streamed once per call.
-__device__ __forceinline__ i32x4_t wload16(const uint8_t* p) {
-  return *reinterpret_cast<const i32x4_t*>(p);
-}
-
 __device__ __forceinline__ i32x8_t gload32(const uint8_t* p) {
   i32x4_t lo = *reinterpret_cast<const i32x4_t*>(p);
   i32x4_t hi = *reinterpret_cast<const i32x4_t*>(p + 16);
-  return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-__device__ __forceinline__ i32x8_t wload32(const uint8_t* p) {
-  i32x4_t lo = wload16(p);
-  i32x4_t hi = wload16(p + 16);
   return i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -311,19 +300,19 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
     if constexpr (WT == WType::kBf16) {
       S.a = gload32(ap);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = wload32(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
     } else if constexpr (WT == WType::kFp8) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = wload32(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = gload32(w_ptr[j] + woff);
 #pragma unroll
       for (int j = 0; j < NI; ++j) S.sb[j] = sb_ptr[j][kt];
     } else if constexpr (kMx) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = wload16(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
       // this lane's 32 elements are scale block 4 kt + lane / 16 of its row
       const int64_t nblk = p.Kred / 32;
 #pragma unroll
@@ -333,7 +322,7 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
 #pragma unroll
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
-      for (int j = 0; j < NI; ++j) S.b[j] = wload16(w_ptr[j] + woff);
+      for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
       // scale and zero of group kt for this lane's column, fetched with the
       // weights so that the stage's loads complete together
       const int64_t gbase = (static_cast<int64_t>(e) * (p.Kred / 128) + kt) * p.Nout;

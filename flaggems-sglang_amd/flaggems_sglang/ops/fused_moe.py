@@ -567,7 +567,7 @@ def fused_experts(
            ``w2_zp [E, N/128, K/2]`` uint8 (two uint4 zeros per byte);
            The same weights tiled by ``quant.tile_int4`` (4-D ``[E, R/16,
            C/128, 1024]``, scales and zeros unchanged) take the decode kernels'
-           contiguous-block loads;
+           contiguous-block loads (MXFP4 likewise, ``quant.tile_mxfp4``);
       mxfp4 (``use_mxfp4_w4a16``): OCP MXFP4 ``w1 [E, 2N, K/2]`` / ``w2 [E, K, N/2]``
            uint8 (two e2m1 per byte, low nibble first), ``w1_scale [E, 2N, K/32]`` /
            ``w2_scale [E, K, N/32]`` e8m0 bytes; bf16 activations (the streaming

@@ -247,7 +247,8 @@ int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale, const void
 
 /* Tile height the library pairs with the GEMM kernels for a problem size:
  * 16 selects the decode (streaming) kernels, 64 / 128 / 256 the prefill kernels.
- * path: 0 = choose, 1 = prefill, 2 = decode (int4 is decode-only). */
+ * path: 0 = choose, 1 = prefill, 2 = decode (4-bit weights always report 16:
+ * their large-batch route dequantizes to bf16 inside fmoe_fused_experts). */
 int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path);
 
 /* Top-k combine (the scatter + sum inside matmul_ogs, ops/fused_moe.py:208-216,
@@ -263,6 +264,11 @@ int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx, int64_t M
  * conversion (ops/fused_moe.py:103-216, :341-350, :399-404) with
  * SGLang-layout weights (no per-call transpose, cf. :326-327).  `path`:
  * 0 = choose, 1 = prefill (LDS-tiled) kernels, 2 = decode (streaming) kernels.
+ * 4-bit weights (int4, MXFP4) run the decode kernels up to an average of 256
+ * slots per expert; above it (or with path 1) the call first dequantizes both
+ * weight tensors to bf16 inside the workspace (fmoe_fused_experts_workspace_bytes
+ * then includes 2 * E * 3 * K * N bytes for them) and runs the bf16 prefill
+ * kernels.
  */
 typedef struct fmoe_fused_args {
   int32_t wtype;

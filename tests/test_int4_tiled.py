@@ -162,3 +162,64 @@ def test_fused_mxfp4_tiled_equals_row_major(M, K, N, E, k):
     ref = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, **kw)
     out = flaggems_sglang.fused_experts(x, Q.tile_mxfp4(q1), Q.tile_mxfp4(q2), tw, ti, **kw)
     assert torch.equal(out, ref)
+
+
+def _w_bf16_from_oracle(fmt, q, s, z):
+    """The weights the large-batch path computes with: the oracle's dequantized
+    values rounded once to bf16 (exact for MXFP4; int4 (q - z) * s is exact in
+    fp32 before that rounding)."""
+    from oracle import fused_moe_oracle as O
+    q, s = q.cpu(), s.cpu()
+    if fmt in ("int4t", "mxfp4t"):
+        q = torch.from_numpy(FO.untile_int4(q.numpy()))
+    if fmt.startswith("int4"):
+        z = z.cpu()
+        w = torch.stack([O.dequant_int4(q[e], s[e], z[e]) for e in range(q.shape[0])])
+    else:
+        w = O.mxfp4_dequant(q, s).float()
+    return w.to(torch.bfloat16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int4", "int4t", "mxfp4", "mxfp4t"])
+def test_large_batch_dequant_path(fmt):
+    """Experts averaging >= 128 slots: the 4-bit weights are dequantized once
+    to bf16 and the bf16 prefill kernels run.  Bit-identical to the bf16 path
+    on the oracle-dequantized weights, within tolerance of the oracle and of
+    the decode kernels (path=2); path=1 forces it at small M."""
+    import flaggems_sglang
+    from flaggems_sglang import quant as Q
+    from oracle import fused_moe_oracle as O
+    M, K, N, E, k = 600, 256, 256, 4, 2
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    if fmt.startswith("int4"):
+        q1, s1, z1 = Q.quantize_int4_group(d["w13"].to(DEV))
+        q2, s2, z2 = Q.quantize_int4_group(d["w2"].to(DEV))
+        if fmt == "int4t":
+            q1, q2 = Q.tile_int4(q1), Q.tile_int4(q2)
+        kw = dict(use_int4_w4a16=True, w1_scale=s1, w2_scale=s2, w1_zp=z1, w2_zp=z2)
+        tol = 5e-2
+    else:
+        q1, s1 = Q.quantize_mxfp4(d["w13"].to(DEV))
+        q2, s2 = Q.quantize_mxfp4(d["w2"].to(DEV))
+        z1 = z2 = None
+        if fmt == "mxfp4t":
+            q1, q2 = Q.tile_mxfp4(q1), Q.tile_mxfp4(q2)
+        kw = dict(use_mxfp4_w4a16=True, w1_scale=s1, w2_scale=s2)
+        tol = 2e-2
+    out = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, **kw)
+    w13b = _w_bf16_from_oracle(fmt, q1, s1, z1).to(DEV)
+    w2b = _w_bf16_from_oracle(fmt, q2, s2, z2).to(DEV)
+    ref_bf16 = flaggems_sglang.fused_experts(x, w13b, w2b, tw, ti, path=1)
+    assert torch.equal(out, ref_bf16)
+    dec = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, path=2, **kw)
+    rel = float((out.float() - dec.float()).norm() / dec.float().norm())
+    assert rel < tol / 4, rel
+    o = O.fused_experts(d["x"], w13b.cpu().float(), w2b.cpu().float(), d["topk_weights"], d["topk_ids"])
+    rel = float((out.float().cpu() - o.float()).norm() / o.float().norm())
+    assert rel < tol / 4, rel
+    # path=1 takes the same route at a decode-sized batch
+    small = flaggems_sglang.fused_experts(x[:5], q1, q2, tw[:5], ti[:5], path=1, **kw)
+    ref_small = flaggems_sglang.fused_experts(x[:5], w13b, w2b, tw[:5], ti[:5], path=1)
+    assert torch.equal(small, ref_small)
