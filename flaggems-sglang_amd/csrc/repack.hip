@@ -156,8 +156,8 @@ __global__ __launch_bounds__(kThreads) void tile_int4_kernel(const i32x4_t* __re
 }
 
 // 4-bit weights -> bf16 [E][R][K] (the large-batch path runs the bf16 prefill
-// kernels on them).  One thread per 16 source bytes = 32 elements of one row,
-// all in one int4 quant group (128) / one MXFP4 scale block (32).  Source
+// kernels on them).  One thread per 8 elements of one row: a 4-byte source
+// load and one 16-byte store, so a wave writes one contiguous KiB.  Source
 // row-major [E][R][K/2] or tiled [E][R/16][K/128][1024] (fmoe_tile_int4).
 //   int4 : w = (q - z) * s in fp32, rounded to bf16 (RNE);
 //   MXFP4: w = e2m1(q) * 2^(s - 127), exact in bf16 (hardware conversion).
@@ -165,58 +165,45 @@ template <bool MX>
 __global__ __launch_bounds__(kThreads) void dequant_4bit_kernel(const uint8_t* __restrict__ q,
                                                                 int tiled, const void* __restrict__ scale,
                                                                 const uint8_t* __restrict__ zeros,
-                                                                int64_t chunks, int64_t R, int64_t K,
+                                                                int64_t units, int64_t R, int64_t K,
                                                                 uint16_t* __restrict__ out) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-  if (idx >= chunks) return;
-  const int64_t cpr = K / 32;  // 16-byte chunks per row
-  int64_t row, ch;            // row over all experts (e * R + r), chunk within the row
-  if (tiled) {
-    // chunk idx of the tiled tensor: ((rowblock * K/128 + c) * 64 + 16 g + r)
-    const int64_t blk = idx / 64, lane = idx % 64;
-    const int64_t rb = blk / (K / 128), c = blk % (K / 128);
-    row = rb * 16 + lane % 16;
-    ch = 4 * c + lane / 16;
-  } else {
-    row = idx / cpr;
-    ch = idx % cpr;
-  }
+  if (idx >= units) return;
+  const int64_t upr = K / 8;       // 8-element units per row
+  const int64_t row = idx / upr;   // over all experts: e * R + r
+  const int64_t m = idx % upr;     // elements 8m .. 8m+7 of the row
   const int64_t e = row / R, r = row % R;
-  const i32x4_t v = reinterpret_cast<const i32x4_t*>(q)[idx];
-  uint32_t w[16];
-  if constexpr (MX) {
-    const uint8_t sb = static_cast<const uint8_t*>(scale)[row * (K / 32) + ch];
-    const float sc = sb == 0 ? 0x1p-127f : (sb == 255 ? __builtin_nanf("") : __uint_as_float(static_cast<uint32_t>(sb) << 23));
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t word = static_cast<uint32_t>(v[d]);
-      w[4 * d + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 0));
-      w[4 * d + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 1));
-      w[4 * d + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 2));
-      w[4 * d + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 3));
-    }
+  int64_t src;                     // byte offset of the unit's 4 source bytes
+  if (tiled) {
+    const int64_t c = m / 16, o = (m % 16) * 4;  // 128-element group, byte in its 64
+    const int64_t rb = row / 16;                 // 16-row block over all experts
+    src = (rb * (K / 128) + c) * 1024 + ((o / 16) * 16 + (row % 16)) * 16 + o % 16;
   } else {
-    const int64_t g = ch / 4;  // quant group of these 32 elements
-    const int64_t gbase = (e * (K / 128) + g) * R;
+    src = row * (K / 2) + 4 * m;
+  }
+  const uint32_t word = *reinterpret_cast<const uint32_t*>(q + src);
+  uint32_t w[4];
+  if constexpr (MX) {
+    const uint8_t sb = static_cast<const uint8_t*>(scale)[row * (K / 32) + m / 4];
+    const float sc = sb == 0 ? 0x1p-127f : (sb == 255 ? __builtin_nanf("") : __uint_as_float(static_cast<uint32_t>(sb) << 23));
+    w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 0));
+    w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 1));
+    w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 2));
+    w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(word, sc, 3));
+  } else {
+    const int64_t gbase = (e * (K / 128) + m / 16) * R;  // quant group m / 16 of expert e
     const float s = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(scale)[gbase + r]));
     const uint8_t zb = zeros[(gbase >> 1) + (r >> 1)];
     const float z = static_cast<float>((r & 1) ? (zb >> 4) : (zb & 15));
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t word = static_cast<uint32_t>(v[d]);
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float lo = (static_cast<float>((word >> (8 * b)) & 15u) - z) * s;
-        const float hi = (static_cast<float>((word >> (8 * b + 4)) & 15u) - z) * s;
-        w[4 * d + b] = f32_to_bf16(lo) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-      }
+    for (int b = 0; b < 4; ++b) {
+      const float lo = (static_cast<float>((word >> (8 * b)) & 15u) - z) * s;
+      const float hi = (static_cast<float>((word >> (8 * b + 4)) & 15u) - z) * s;
+      w[b] = f32_to_bf16(lo) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
     }
   }
-  i32x4_t* dst = reinterpret_cast<i32x4_t*>(out + row * K + 32 * ch);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    dst[i] = i32x4_t{static_cast<int>(w[4 * i]), static_cast<int>(w[4 * i + 1]),
-                     static_cast<int>(w[4 * i + 2]), static_cast<int>(w[4 * i + 3])};
+  *reinterpret_cast<i32x4_t*>(out + row * K + 8 * m) =
+      i32x4_t{static_cast<int>(w[0]), static_cast<int>(w[1]), static_cast<int>(w[2]), static_cast<int>(w[3])};
 }
 
 }  // namespace repack
@@ -298,15 +285,15 @@ int dequant_4bit(int wtype, const void* q, const void* scale, const void* zeros,
   const int tiled = wtype == FMOE_W_INT4_TILED || wtype == FMOE_W_MXFP4_TILED;
   if (!q || !scale || (!mx && !zeros) || !out) return fmoe_host::fail(FMOE_ERR_INVALID, "dequant: null pointer");
   if (R % 16 || K % 128) return fmoe_host::fail(FMOE_ERR_INVALID, "dequant: R %% 16 / K %% 128");
-  const int64_t chunks = E * R * (K / 32);
-  const int64_t blocks = (chunks + kThreads - 1) / kThreads;
+  const int64_t units = E * R * (K / 8);
+  const int64_t blocks = (units + kThreads - 1) / kThreads;
   if (blocks > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "dequant: tensor too large");
   if (mx)
     dequant_4bit_kernel<true><<<static_cast<unsigned>(blocks), kThreads, 0, s>>>(
-        static_cast<const uint8_t*>(q), tiled, scale, nullptr, chunks, R, K, out);
+        static_cast<const uint8_t*>(q), tiled, scale, nullptr, units, R, K, out);
   else
     dequant_4bit_kernel<false><<<static_cast<unsigned>(blocks), kThreads, 0, s>>>(
-        static_cast<const uint8_t*>(q), tiled, scale, static_cast<const uint8_t*>(zeros), chunks, R, K, out);
+        static_cast<const uint8_t*>(q), tiled, scale, static_cast<const uint8_t*>(zeros), units, R, K, out);
   return fmoe_host::check_launch("dequant_4bit");
 }
 }  // namespace fmoe
