@@ -317,7 +317,6 @@ int check_fused(const fmoe_fused_args* a) {
     return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: int4 group_size=%d is not supported",
                 a->group_size);
   if (a->path < 0 || a->path > 2) return fail(FMOE_ERR_INVALID, "fused_experts: path %d", a->path);
-  if (a->M > 65535) return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: M > 65535 is not supported");
   fmoe_epilogue ep{a->activation, a->b13, a->alpha, a->limit};
   if (int st = check_epilogue(&ep, "fused_experts")) return st;
   return FMOE_OK;
@@ -438,14 +437,22 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
 // MXFP4 M=1024 2.81 vs 2.14 ms.
 constexpr int64_t kDequantMinSlots = 256;
 
-bool dequant_prefill(const fmoe_fused_args* a) {
-  if (!decode_only(a->wtype) || a->path == 2) return false;
-  return a->path == 1 || a->M * a->top_k >= kDequantMinSlots * a->E;
-}
+// The bf16 copies live in the caller's workspace for the duration of the
+// call (2 * E * 3 * N * K bytes: 2.8 GB for the Mixtral shape), so the route is
+// taken automatically only while they stay within kDequantMaxBytes; above it
+// (e.g. a DeepSeek-size int4 layer, ~22 GB) the decode kernels run at every M.
+// path = 1 asks for the route regardless of the size.
+constexpr size_t kDequantMaxBytes = size_t(4) << 30;
 
 // bytes of the bf16 copies of w13 and w2
 size_t dequant_bytes(const fmoe_fused_args* a) {
   return al(2 * static_cast<size_t>(a->E) * 2 * a->N * a->K) + al(2 * static_cast<size_t>(a->E) * a->K * a->N);
+}
+
+bool dequant_prefill(const fmoe_fused_args* a) {
+  if (!decode_only(a->wtype) || a->path == 2) return false;
+  if (a->path == 1) return true;
+  return a->M * a->top_k >= kDequantMinSlots * a->E && dequant_bytes(a) <= kDequantMaxBytes;
 }
 
 // The same call on bf16 copies of the weights placed at the workspace start.
@@ -569,3 +576,4 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   return fmoe_moe_sum(static_cast<const float*>(at(L.y)), L.splits, o.gate_indx, a->M, a->top_k,
                       a->K, a->routed_scaling_factor, a->out, stream);
 }
+

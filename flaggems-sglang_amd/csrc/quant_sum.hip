@@ -52,38 +52,40 @@ __global__ __launch_bounds__(256) void moe_sum_kernel(const YT* __restrict__ y, 
                                                       int64_t split_stride,
                                                       const int32_t* __restrict__ gate_indx,
                                                       const int32_t* __restrict__ ids, int n_experts,
-                                                      int k, int64_t K, float scale,
+                                                      int64_t n_tok, int k, int64_t K, float scale,
                                                       uint16_t* __restrict__ out) {
-  const int64_t t = blockIdx.y;
   const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (c >= K) return;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  for (int j = 0; j < k; ++j) {
-    // tiny-batch path (gate_indx null): slot = flat index, dropped when its
-    // expert id is out of range
-    const int s = gate_indx ? gate_indx[t * k + j]
-                            : (ids[t * k + j] >= 0 && ids[t * k + j] < n_experts ? static_cast<int>(t * k + j) : -1);
-    if (s < 0) continue;  // slot routed to no expert
-    for (int p = 0; p < splits; ++p) {
-      const YT* src = y + p * split_stride + static_cast<int64_t>(s) * K + c;
-      if constexpr (sizeof(YT) == 4) {
-        const float4 v = *reinterpret_cast<const float4*>(src);
-        a0 += v.x;
-        a1 += v.y;
-        a2 += v.z;
-        a3 += v.w;
-      } else {  // bf16 rows
-        const uint2 v = *reinterpret_cast<const uint2*>(src);
-        a0 += __uint_as_float(v.x << 16);
-        a1 += __uint_as_float(v.x & 0xffff0000u);
-        a2 += __uint_as_float(v.y << 16);
-        a3 += __uint_as_float(v.y & 0xffff0000u);
+  // tokens t = blockIdx.y, blockIdx.y + gridDim.y, ... (grid y is capped at 65535)
+  for (int64_t t = blockIdx.y; t < n_tok; t += gridDim.y) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (int j = 0; j < k; ++j) {
+      // tiny-batch path (gate_indx null): slot = flat index, dropped when its
+      // expert id is out of range
+      const int s = gate_indx ? gate_indx[t * k + j]
+                              : (ids[t * k + j] >= 0 && ids[t * k + j] < n_experts ? static_cast<int>(t * k + j) : -1);
+      if (s < 0) continue;  // slot routed to no expert
+      for (int p = 0; p < splits; ++p) {
+        const YT* src = y + p * split_stride + static_cast<int64_t>(s) * K + c;
+        if constexpr (sizeof(YT) == 4) {
+          const float4 v = *reinterpret_cast<const float4*>(src);
+          a0 += v.x;
+          a1 += v.y;
+          a2 += v.z;
+          a3 += v.w;
+        } else {  // bf16 rows
+          const uint2 v = *reinterpret_cast<const uint2*>(src);
+          a0 += __uint_as_float(v.x << 16);
+          a1 += __uint_as_float(v.x & 0xffff0000u);
+          a2 += __uint_as_float(v.y << 16);
+          a3 += __uint_as_float(v.y & 0xffff0000u);
+        }
       }
     }
+    const uint32_t w0 = f32_to_bf16(a0 * scale) | (static_cast<uint32_t>(f32_to_bf16(a1 * scale)) << 16);
+    const uint32_t w1 = f32_to_bf16(a2 * scale) | (static_cast<uint32_t>(f32_to_bf16(a3 * scale)) << 16);
+    *reinterpret_cast<uint2*>(out + t * K + c) = make_uint2(w0, w1);
   }
-  const uint32_t w0 = f32_to_bf16(a0 * scale) | (static_cast<uint32_t>(f32_to_bf16(a1 * scale)) << 16);
-  const uint32_t w1 = f32_to_bf16(a2 * scale) | (static_cast<uint32_t>(f32_to_bf16(a3 * scale)) << 16);
-  *reinterpret_cast<uint2*>(out + t * K + c) = make_uint2(w0, w1);
 }
 
 }  // namespace fmoe
@@ -116,12 +118,10 @@ extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx
   if (M < 0 || k < 1 || K <= 0 || K % 4 != 0 || splits < 1)
     return fail(FMOE_ERR_INVALID, "moe_sum: need K %% 4 == 0, k >= 1, splits >= 1");
   if (M == 0) return FMOE_OK;
-  if (M > 65535) return fail(FMOE_ERR_UNSUPPORTED, "moe_sum: M=%lld > 65535 is not supported",
-                             static_cast<long long>(M));
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
-  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
+  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M < 65535 ? M : 65535)), b(256);
   moe_sum_kernel<float><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
-      y, splits, M * k * K, gate_indx, nullptr, 0, k, K, scale, static_cast<uint16_t*>(out));
+      y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 
@@ -129,17 +129,17 @@ namespace fmoe {
 // moe_sum of the tiny-batch decode path: y rows are flat slots (t * k + j).
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
-  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
-  moe_sum_kernel<float><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, k, K, scale,
+  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M < 65535 ? M : 65535)), b(256);
+  moe_sum_kernel<float><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
                                         static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 // moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
-  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M)), b(256);
+  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M < 65535 ? M : 65535)), b(256);
   moe_sum_kernel<__bf16><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
-                                         nullptr, 0, k, K, scale, static_cast<uint16_t*>(out));
+                                         nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 }  // namespace fmoe

@@ -214,11 +214,10 @@ def _expt_data_for(routing_data: RoutingData, n_slots: int, block_m: int):
     n_tiles = torch.empty(1, **i32)
     check(L.fmoe_expt_data(ptr(hist), E, n_slots, block_m, ptr(offs_raw), ptr(offs_pad),
                            ptr(tile_map), ptr(n_tiles), stream_of(hist)), "expt_data")
-    if ed is not None and hasattr(ed, "block_pid_map") and isinstance(ed.block_pid_map, dict):
+    if isinstance(ed, ExptData):  # cache on this package's own containers only
         ed.token_offs_pad[block_m] = offs_pad
         ed.block_pid_map[block_m] = tile_map
-        if isinstance(getattr(ed, "n_tiles", None), dict):
-            ed.n_tiles[block_m] = n_tiles
+        ed.n_tiles[block_m] = n_tiles
     return offs_raw, offs_pad, tile_map, n_tiles
 
 
@@ -308,10 +307,17 @@ def _weight_dims(w, wtype):
 def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens, top_k,
                 n_experts, topk_indx, gate_indx, gate_scal, offs_raw, offs_pad, tile_map, n_tiles,
                 block_m, apply_router_weight_on_input, scale, combine=True, act=_lib.ACT_SILU,
-                b13=None, b2=None, alpha=1.0, limit=0.0):
+                b13=None, b2=None, alpha=1.0, limit=0.0, slot_order=None):
     """GEMM1+activation -> GEMM2 -> top-k sum on prepared routing, SGLang
     layouts ``w13 [E, 2N, K]``, ``w2 [E, K, N]``; ``b13 [E, 2N]`` / ``b2 [E, K]``
-    fp32 biases (bias path)."""
+    fp32 biases (bias path).
+
+    ``combine=False`` returns the per-slot rows ``[M, k, K]`` bf16 instead of
+    their sum: row ``(t, j)`` is token t's j-th slot in the routing's flat
+    order (each token's experts ascending, the order of ``expt_indx``), or,
+    with ``slot_order [M, k]`` (the rank of original column j in that order),
+    token t's choice ``topk_ids[t, j]``.  A slot whose expert was dropped
+    (expert map) is zero."""
     L = lib()
     M, K = x.shape
     N = _weight_dims(w2, wtype)[2]
@@ -341,9 +347,14 @@ def _run_stages(x, w13, w2, wtype, w13_scale, w2_scale, w13_zp, w2_zp, n_tokens,
                           ctypes.byref(r), int(not apply_router_weight_on_input), ptr(b2), ptr(y),
                           splits, 0, st), "gemm2")
     if not combine:
-        # per-slot rows, token-major (each token's experts ascending)
-        yy = y.sum(0) if splits > 1 else y[0]
-        return yy.index_select(0, gate_indx.long()).view(n_tokens, top_k, K).to(torch.bfloat16)
+        # per-slot rows: moe_sum over "tokens" = slots with one choice each
+        # (split planes summed in fixed order, dropped slots -> 0)
+        g = gate_indx if slot_order is None else \
+            gate_indx.view(n_tokens, top_k).gather(1, slot_order).contiguous()
+        per = torch.empty(n_tokens * top_k, K, dtype=torch.bfloat16, device=dev)
+        check(L.fmoe_moe_sum(ptr(y), splits, ptr(g), n_tokens * top_k, 1, K, 1.0, ptr(per), st),
+              "moe_sum")
+        return per.view(n_tokens, top_k, K)
     out = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
     check(L.fmoe_moe_sum(ptr(y), splits, ptr(gate_indx), M, top_k, K, float(scale), ptr(out), st),
           "moe_sum")
@@ -526,9 +537,6 @@ def _pcg_scale(pcg, name):
 # ---------------------------------------------------------------------------
 # plain-tensor entry point (SGLang fused_experts style, SGLang layouts)
 # ---------------------------------------------------------------------------
-_ws_cache: dict = {}
-
-
 def fused_experts(
     hidden_states: torch.Tensor,
     w1: torch.Tensor,
@@ -608,12 +616,15 @@ def fused_experts(
         assert expert_map.numel() == n_global, "expert_map must have global_num_experts entries"
         emap = _ids_i32(expert_map.view(1, -1)).view(-1)
     if no_combine:
+        # SGLang's no_combine contract: [M, k, K] with slot (t, j) = the
+        # expert topk_ids[t, j] (routed_scaling_factor not applied, as in the
+        # reference hook, ops/fused_moe.py:399-404)
         a = _align(topk_weights, topk_ids, E, lib().fmoe_choose_block_m(wtype, M, k, E, path), False,
                    expert_map=emap)
         return _run_stages(x, w1, w2, wtype, w1_scale, w2_scale, w1_zp, w2_zp, M, k, E,
                            a.topk_indx, a.gate_indx, a.gate_scal, a.offs_raw, a.offs_pad, a.tile_map,
                            a.n_tiles, a.block_m, apply_router_weight_on_input, 1.0, combine=False,
-                           act=act)
+                           act=act, slot_order=_slot_order(topk_ids, emap))
     ids = _ids_i32(topk_ids)
     tw = topk_weights.float().contiguous()
     out = torch.empty(M, K, dtype=torch.bfloat16, device=x.device)
@@ -624,7 +635,9 @@ def fused_experts(
     L = lib()
     nbytes = L.fmoe_fused_experts_workspace_bytes(ctypes.byref(args))
     if nbytes == 0:
+        # the size query refuses invalid arguments: run the call for its error
         check(L.fmoe_fused_experts(ctypes.byref(args), stream_of(x)), "fused_experts")
+        raise RuntimeError("fused_experts: workspace query failed")
     ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     args.workspace = ptr(ws)
     args.workspace_bytes = nbytes
@@ -632,9 +645,38 @@ def fused_experts(
     return out
 
 
+def _slot_order(topk_ids: torch.Tensor, emap: Optional[torch.Tensor]) -> torch.Tensor:
+    """[M, k] int64: the position of column j of ``topk_ids`` in its row after
+    the stable per-row sort by (local) expert id that the routing applies
+    (ops/fused_moe.py:113; ids dropped by the expert map sort as -1)."""
+    ids = topk_ids.long()
+    if emap is not None:
+        ok = (ids >= 0) & (ids < emap.numel())
+        ids = torch.where(ok, emap.long()[ids.clamp(0, emap.numel() - 1)], torch.full_like(ids, -1))
+    order = torch.sort(ids, dim=1, stable=True).indices
+    return torch.argsort(order, dim=1)
+
+
 # ---------------------------------------------------------------------------
 # SGLang runner hook
 # ---------------------------------------------------------------------------
+def _is_triton_routing(topk_output) -> bool:
+    """SGLang's TopKOutputChecker.format_is_triton_kernels (ops/fused_moe.py:339),
+    by structure rather than class: a ``(routing_data, gather_indx,
+    scatter_indx)`` triple whose routing data has the triton_kernels
+    ``RoutingData`` fields and whose indices have ``src_indx`` / ``dst_indx``
+    (SGLang's TritonKernelTopKOutput, this package's own containers, or any
+    other object with those fields)."""
+    fmt = getattr(topk_output, "format", None)
+    if fmt is not None and getattr(fmt, "name", None) == "TRITON_KERNEL":
+        return True
+    if not isinstance(topk_output, (tuple, list)) or len(topk_output) != 3:
+        return False
+    rd, gi, si = topk_output
+    return (all(hasattr(rd, f) for f in ("gate_scal", "expt_hist", "n_expts_tot", "n_expts_act"))
+            and all(hasattr(o, f) for o in (gi, si) for f in ("src_indx", "dst_indx")))
+
+
 def _combine_input(hidden_states):
     try:
         from sglang.srt.layers.moe.token_dispatcher.standard import StandardCombineInput
@@ -703,7 +745,7 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
             # matmul_ogs orientation views of the SGLang-layout scales (no copy)
             pcg13 = SimpleNamespace(weight_scale=quant["w1_scale"].transpose(-1, -2))
             pcg2 = SimpleNamespace(weight_scale=quant["w2_scale"].transpose(-1, -2))
-        if isinstance(topk_output, tuple) and len(topk_output) == 3 and isinstance(topk_output[0], RoutingData):
+        if _is_triton_routing(topk_output):
             routing_data, gather_indx, scatter_indx = topk_output
         else:
             routing_data, gather_indx, scatter_indx = _standard_topk_to_triton_kernels(
@@ -715,7 +757,7 @@ def fused_moe_flagos(obj, layer: torch.nn.Module, dispatch_output):
             gemm1_clamp_limit=getattr(cfg, "gemm1_clamp_limit", None))
         if scale is not None:
             out.mul_(scale)
-    elif isinstance(topk_output, tuple) and len(topk_output) == 3 and isinstance(topk_output[0], RoutingData):
+    elif _is_triton_routing(topk_output):
         routing_data, gather_indx, scatter_indx = topk_output
         assert not quant.get("use_int4_w4a16"), _UNSUPPORTED_FEATURE_MSG.format(
             name="int4 with triton_kernels routing")
