@@ -1,4 +1,6 @@
 // C-ABI entry points of the GEMM stages and the whole fused path.
+#include <mutex>
+
 #include "gemm.hpp"
 
 namespace fmoe {
@@ -577,3 +579,53 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
                       a->K, a->routed_scaling_factor, a->out, stream);
 }
 
+// ------------------------------------------------ no-allocation entry point
+namespace fmoe {
+// The workspace of fmoe_fused_experts_noalloc: one copy per GPU, in the code
+// object's device memory.  Host code never uses this name as an address (it
+// is a host-side stand-in): the device address comes from
+// hipGetSymbolAddress, once per device.
+__device__ __align__(256) char scratch[FMOE_NOALLOC_SCRATCH_BYTES];
+}  // namespace fmoe
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices];
+
+// Device address of the current device's scratch array (looked up on the
+// first call on that device).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FMOE_ERR_HIP, "fused_experts_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(FMOE_ERR_UNSUPPORTED, "fused_experts_noalloc: device %d is not supported", dev);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(fmoe::scratch));
+    if (e != hipSuccess || !p)
+      return fail(FMOE_ERR_HIP, "fused_experts_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return FMOE_OK;
+}
+}  // namespace
+
+extern "C" int fmoe_fused_experts_noalloc(const fmoe_fused_args* a, void* stream) {
+  if (int st = check_fused(a)) return st;
+  const size_t need = fmoe_fused_experts_workspace_bytes(a);
+  if (need > FMOE_NOALLOC_SCRATCH_BYTES)
+    return fail(FMOE_ERR_UNSUPPORTED,
+                "fused_experts_noalloc: this call needs %zu bytes of workspace, above the %zu-byte "
+                "scratch maximum (use fmoe_fused_experts with a caller workspace)",
+                need, static_cast<size_t>(FMOE_NOALLOC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  if (int st = scratch_for_current_device(&ws)) return st;
+  fmoe_fused_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = FMOE_NOALLOC_SCRATCH_BYTES;
+  return fmoe_fused_experts(&b, stream);
+}

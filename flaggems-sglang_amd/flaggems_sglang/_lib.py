@@ -98,6 +98,7 @@ _SIGS = {
                                     ctypes.c_float, vp, vp]),
     "fmoe_fused_experts_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(FusedArgs)]),
     "fmoe_fused_experts": (ctypes.c_int, [ctypes.POINTER(FusedArgs), vp]),
+    "fmoe_fused_experts_noalloc": (ctypes.c_int, [ctypes.POINTER(FusedArgs), vp]),
     "fmoe_repack_int4": (ctypes.c_int, [ctypes.c_int, vp, vp, vp, ctypes.c_int64, ctypes.c_int64,
                                         ctypes.c_int64, ctypes.c_int, vp, vp, vp, vp, vp]),
     "fmoe_tile_int4": (ctypes.c_int, [vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp]),

@@ -303,6 +303,20 @@ typedef struct fmoe_fused_args {
 size_t fmoe_fused_experts_workspace_bytes(const fmoe_fused_args* a);
 int fmoe_fused_experts(const fmoe_fused_args* a, void* stream);
 
+/* fmoe_fused_experts without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace is a library-owned device array of FMOE_NOALLOC_SCRATCH_BYTES
+ * per GPU (held until the process ends; a->workspace / workspace_bytes are
+ * ignored), looked up once per device with the calling thread's current
+ * device, which must be the device of the tensors.  Calls whose workspace
+ * query exceeds the maximum fail with FMOE_ERR_UNSUPPORTED (e.g. 4-bit
+ * weights on the large-batch dequantize route: pass path = 2).  The kernels
+ * need no zeroed scratch.  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (different streams, threads) race. */
+#define FMOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int fmoe_fused_experts_noalloc(const fmoe_fused_args* a, void* stream);
+
 /* ------------------------------------------------ checkpoint weight formats
  * Load-time repack of int4 MoE checkpoints into the FMOE_W_INT4 layout, once
  * per weight instead of per call (the reference re-lays weights out on every

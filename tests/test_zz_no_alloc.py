@@ -1,0 +1,93 @@
+"""fmoe_fused_experts_noalloc (the workspace is the library's per-GPU scratch
+array) against fmoe_fused_experts (caller workspace), through the C ABI:
+identical outputs, bit for bit, on two calls in a row, the second with a
+smaller input; plus the size limit and the no-allocation property (torch's
+caching allocator is not touched by the call)."""
+
+import ctypes
+
+import pytest
+import torch
+
+from flaggems_sglang import _lib
+from flaggems_sglang import quant as Q
+from oracle import fused_moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _args(wtype, x, w13, w2, tw, ti, out, s13=None, s2=None, z13=None, z2=None, path=0):
+    M, K = x.shape
+    E, k = w13.shape[0], ti.shape[1]
+    N = w2.shape[2] * (2 if wtype == _lib.W_INT4 else 1)
+    return _lib.FusedArgs(
+        wtype, x.data_ptr(), M, K, N, E, k, w13.data_ptr(), w2.data_ptr(), _lib.ptr(s13),
+        _lib.ptr(s2), _lib.ptr(z13), _lib.ptr(z2), 128, tw.data_ptr(), ti.data_ptr(), 0, 1.0, path,
+        out.data_ptr(), None, 0, _lib.ACT_SILU, None, None, 1.0, 0.0, None, 0)
+
+
+def _both(wtype, x, w13, w2, tw, ti, **kw):
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    ref = torch.empty(x.shape[0], x.shape[1], dtype=torch.bfloat16, device=DEV)
+    a = _args(wtype, x, w13, w2, tw, ti, ref, **kw)
+    nbytes = L.fmoe_fused_experts_workspace_bytes(ctypes.byref(a))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+    _lib.check(L.fmoe_fused_experts(ctypes.byref(a), st), "fused_experts")
+    out = torch.full_like(ref, float("nan"))
+    b = _args(wtype, x, w13, w2, tw, ti, out, **kw)
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_stats().get("allocation.all.allocated", 0)
+    _lib.check(L.fmoe_fused_experts_noalloc(ctypes.byref(b), st), "fused_experts_noalloc")
+    after = torch.cuda.memory_stats().get("allocation.all.allocated", 0)
+    torch.cuda.synchronize()
+    assert before == after
+    return out, ref
+
+
+def _inputs(M, K, N, E, k):
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05)
+    return [d[n].to(DEV) for n in ("x", "w13", "w2", "topk_weights", "topk_ids")]
+
+
+@pytest.mark.parametrize("Ms", [(300, 40), (16, 3)])
+def test_noalloc_bf16_matches(Ms):
+    """Prefill-sized then smaller (300 -> 40 tokens) and decode-sized
+    (16 -> 3: in-workgroup routing) calls back to back on the shared array."""
+    for M in Ms:
+        x, w13, w2, tw, ti = _inputs(M, 512, 384, 16, 4)
+        out, ref = _both(_lib.W_BF16, x, w13, w2, tw, ti)
+        assert torch.equal(out, ref)
+
+
+def test_noalloc_fp8_and_int4_match():
+    for M in (200, 5):
+        x, w13, w2, tw, ti = _inputs(M, 512, 256, 8, 2)
+        q1, s1 = Q.quantize_fp8_block(w13)
+        q2, s2 = Q.quantize_fp8_block(w2)
+        out, ref = _both(_lib.W_FP8, x, q1, q2, tw, ti, s13=s1, s2=s2)
+        assert torch.equal(out, ref)
+        i1, c1, z1 = Q.quantize_int4_group(w13)
+        i2, c2, z2 = Q.quantize_int4_group(w2)
+        out, ref = _both(_lib.W_INT4, x, i1, i2, tw, ti, s13=c1, s2=c2, z13=z1, z2=z2)
+        assert torch.equal(out, ref)
+
+
+def test_noalloc_rejects_oversized():
+    """A call whose workspace exceeds the scratch maximum is refused with
+    FMOE_ERR_UNSUPPORTED before anything runs."""
+    M, K, N, E, k = 4096, 1024, 4096, 8, 2
+    x = torch.zeros(M, K, dtype=torch.bfloat16, device=DEV)
+    w13 = torch.zeros(E, 2 * N, K, dtype=torch.bfloat16, device=DEV)
+    w2 = torch.zeros(E, K, N, dtype=torch.bfloat16, device=DEV)
+    tw = torch.full((M, k), 0.5, device=DEV)
+    ti = torch.zeros(M, k, dtype=torch.int32, device=DEV)
+    out = torch.empty(M, K, dtype=torch.bfloat16, device=DEV)
+    a = _args(_lib.W_BF16, x, w13, w2, tw, ti, out)
+    L = _lib.lib()
+    assert L.fmoe_fused_experts_workspace_bytes(ctypes.byref(a)) > (64 << 20)
+    rc = L.fmoe_fused_experts_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.FMOE_ERR_UNSUPPORTED
+    assert b"scratch maximum" in L.fmoe_last_error()
