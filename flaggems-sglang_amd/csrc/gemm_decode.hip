@@ -81,8 +81,7 @@ template <>
 struct Stage<WType::kInt4> {
   i32x4_t a[4];   // 32 bf16 of the activation row
   i32x4_t b[NI];  // 32 uint4 of each weight row
-  uint16_t sc[NI];  // fp16 group scale of this lane's column
-  uint8_t zb[NI];   // byte holding the group zero of this lane's column
+  int meta;       // one dword of the wave's group scales / zeros (see int4_meta)
 };
 
 template <>
@@ -97,7 +96,15 @@ struct Stage<WType::kMxfp4> {
 // the align launch, e.g. DSV3 M = 128, one stage and twice the occupancy is
 // 7% faster.  MXFP4: two, 3-5% faster at M = 16 (its e2m1 conversions hide
 // the second stage), even at M = 1.  bf16 / int4: one.)
+#ifndef FMOE_DECODE_PIPE_INT4
+#define FMOE_DECODE_PIPE_INT4 1
+#endif
+#ifndef FMOE_DECODE_ROTATE_INT4
+#define FMOE_DECODE_ROTATE_INT4 1
+#endif
+constexpr bool kRotateInt4 = FMOE_DECODE_ROTATE_INT4 != 0;
 constexpr int pipe_depth(WType wt, Mode mode, bool tiny) {
+  if (wt == WType::kInt4) return FMOE_DECODE_PIPE_INT4;
   return (wt == WType::kFp8 && mode == Mode::kGemm1Silu && tiny) || wt == WType::kMxfp4 ? 2 : 1;
 }
 
@@ -190,7 +197,7 @@ __device__ bool tiny_route(const GemmParams& p, int mt, TinyLds& L) {
 }
 
 template <WType WT, Mode MODE, int PIPE, int ACT, bool TINY, int RB>
-__global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p) {
+__global__ __launch_bounds__(kThreads * RB, (WT == WType::kInt4 && PIPE == 1 && kRotateInt4) ? 4 : 1) void gemm_decode_kernel(GemmParams p) {
   __shared__ f32x4_t red[RB][kWaves][NI][kWave];
   __shared__ TinyLds tiny_lds[1];  // used by the TINY variant only
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
@@ -290,6 +297,38 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
     for (int j = 0; j < NI; ++j) sb_ptr[j] = se + (wrow[j] / 128) * ksb;
   }
 
+  // int4 group scales / zeros of the wave's 64 weight rows: one dword load per
+  // lane and stage instead of 2 x NI sub-dword loads.  Virtual row v = 16 j +
+  // r (r = lane % 16: the lane's row in block j).  Lanes 0-31 read the fp16
+  // scales of rows v = 2 d, 2 d + 1 (d = lane), lanes 32-39 the uint4 zeros of
+  // rows 8 z .. 8 z + 7 (z = lane - 32); consume() fetches each lane's values
+  // with ds_bpermute.  Rows 2d / 8z start even / 8-aligned blocks of the
+  // layout's rows, so the dwords are aligned.
+  const uint8_t* meta_ptr = nullptr;
+  int64_t meta_stride = 0;
+  if constexpr (WT == WType::kInt4) {
+    const int ln = lane < 32 ? lane : (lane < 40 ? lane - 32 : 0);
+    const int j = lane < 32 ? ln / 8 : ln / 2;
+    const int r = lane < 32 ? (2 * ln) % 16 : 8 * (ln % 2);
+    int64_t row;
+    if (MODE == Mode::kGemm1Silu) {
+      int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + r;
+      if (jj >= p.N_act) jj = p.N_act - 8;
+      row = gemm1_row(ACT, p.N_act, jj, j < NI / 2 ? 0 : 1);
+    } else {
+      row = static_cast<int64_t>(nt) * BN + j * 16 + r;
+      if (row >= p.Nout) row = p.Nout - 8;
+    }
+    const int64_t ebase = static_cast<int64_t>(e) * (p.Kred / 128) * p.Nout + row;
+    if (lane < 32) {
+      meta_ptr = reinterpret_cast<const uint8_t*>(p.b_gscale) + 2 * ebase;
+      meta_stride = 2 * p.Nout;
+    } else {
+      meta_ptr = p.b_zero + (ebase >> 1);
+      meta_stride = p.Nout / 2;
+    }
+  }
+
   f32x4_t acc[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -323,14 +362,10 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
       for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
 #pragma unroll
       for (int j = 0; j < NI; ++j) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
-      // scale and zero of group kt for this lane's column, fetched with the
-      // weights so that the stage's loads complete together
-      const int64_t gbase = (static_cast<int64_t>(e) * (p.Kred / 128) + kt) * p.Nout;
-#pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        S.sc[j] = p.b_gscale[gbase + wrow[j]];
-        S.zb[j] = p.b_zero[(gbase >> 1) + (wrow[j] >> 1)];
-      }
+      // scales and zeros of group kt, fetched with the weights so that the
+      // stage's loads complete together
+      S.meta = 0;
+      if (lane < 40) S.meta = *reinterpret_cast<const int*>(meta_ptr + kt * meta_stride);
     }
   };
 
@@ -437,12 +472,16 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
           t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b0, b1, b2, b3), t[j], 0, 0, 0);
         }
       }
-      // fold zero and scale of group kt for this lane's column
+      // fold zero and scale of group kt for this lane's column (row r of
+      // block j: scale half r % 2 of lane 8 j + r / 2's dword, zero nibble
+      // r % 8 of lane 32 + 2 j + r / 8's dword)
+      const int r16 = lane & 15;
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, S.sc[j]));
-        const unsigned zb = S.zb[j];
-        const float z = static_cast<float>((wrow[j] & 1) ? (zb >> 4) : (zb & 15));
+        const unsigned sw = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), S.meta));
+        const unsigned zw = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), S.meta));
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw >> 16) : (sw & 0xffffu))));
+        const float z = static_cast<float>((zw >> (4 * (r16 & 7))) & 15u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[j][r] - (128.0f + z) * xs[r]);
       }
@@ -467,6 +506,68 @@ __global__ __launch_bounds__(kThreads * RB) void gemm_decode_kernel(GemmParams p
       if (k2 < k_end) load(k2, s0);
       consume(k1, s1);
       kt = k2;
+    }
+  } else if constexpr (WT == WType::kInt4 && kRotateInt4) {
+    // One stage of registers, reloaded piecewise as soon as each piece has
+    // been consumed: the scale / zero dword right after it is spread with
+    // ds_bpermute, each weight row block right after its MFMAs, the
+    // activations (an L2 hit) after the last MFMA.  The next stage's loads then overlap
+    // this stage's arithmetic without a second set of stage registers (which
+    // would cost a wave per SIMD of occupancy).
+    Stage<WT> S;
+    int kt = k_beg + kw;
+    const int64_t a_step = static_cast<int64_t>(kWaves) * kElems * 2;  // activation bytes per step
+    const int64_t w_step = static_cast<int64_t>(kWaves) * w_stride;
+    const uint8_t* ap = a_ptr + static_cast<int64_t>(kt) * kElems * 2 + lane_off_a;
+    const uint8_t* mp = meta_ptr + kt * meta_stride;
+    int64_t woff = static_cast<int64_t>(kt) * w_stride;
+    if (kt < k_end) load(kt, S);
+    const int r16 = lane & 15;
+    const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
+    for (; kt < k_end; kt += kWaves) {
+      const bool more = kt + kWaves < k_end;
+      ap += a_step;
+      mp += kWaves * meta_stride;
+      woff += w_step;
+      unsigned sw[NI], zw[NI];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        sw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), S.meta));
+        zw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), S.meta));
+      }
+      if (more && lane < 40) S.meta = *reinterpret_cast<const int*>(mp);
+      // activations of nibble dword d, permuted to the (j, j+4) pairing
+      bf16x8_t a[4];
+      f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int x01 = S.a[d][0], x23 = S.a[d][1], x45 = S.a[d][2], x67 = S.a[d][3];
+        a[d] = as_bf16x8(__builtin_amdgcn_perm(x45, x01, 0x05040100), __builtin_amdgcn_perm(x45, x01, 0x07060302),
+                         __builtin_amdgcn_perm(x67, x23, 0x05040100), __builtin_amdgcn_perm(x67, x23, 0x07060302));
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], ones, xs, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const unsigned wv = static_cast<unsigned>(S.b[j][d]);
+          const int b0 = static_cast<int>((wv & 0x000f000fu) | 0x43004300u);
+          const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
+          const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
+          const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
+        }
+        if (more) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw[j] >> 16) : (sw[j] & 0xffffu))));
+        const float z = static_cast<float>((zw[j] >> (4 * (r16 & 7))) & 15u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[r] - (128.0f + z) * xs[r]);
+      }
+      if (more) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+      }
     }
   } else {
     for (int kt = k_beg + kw; kt < k_end; kt += kWaves) {

@@ -47,13 +47,17 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
 
 // out[t, c] = bf16(scale * sum_j sum_p y[p][gate_indx[t*k+j], c]); j then p
 // in ascending order.  One thread = 4 columns (16-byte loads).
+// out[t] = bf16(scale * sum over the token's k slots, then over the split
+// planes, in that fixed order).
+constexpr int kSumThreads = 256;
+
 template <typename YT>
-__global__ __launch_bounds__(256) void moe_sum_kernel(const YT* __restrict__ y, int splits,
-                                                      int64_t split_stride,
-                                                      const int32_t* __restrict__ gate_indx,
-                                                      const int32_t* __restrict__ ids, int n_experts,
-                                                      int64_t n_tok, int k, int64_t K, float scale,
-                                                      uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restrict__ y, int splits,
+                                                              int64_t split_stride,
+                                                              const int32_t* __restrict__ gate_indx,
+                                                              const int32_t* __restrict__ ids, int n_experts,
+                                                              int64_t n_tok, int k, int64_t K, float scale,
+                                                              uint16_t* __restrict__ out) {
   const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (c >= K) return;
   // tokens t = blockIdx.y, blockIdx.y + gridDim.y, ... (grid y is capped at 65535)
@@ -119,7 +123,7 @@ extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx
     return fail(FMOE_ERR_INVALID, "moe_sum: need K %% 4 == 0, k >= 1, splits >= 1");
   if (M == 0) return FMOE_OK;
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
-  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M < 65535 ? M : 65535)), b(256);
+  dim3 g(static_cast<unsigned>((K / 4 + kSumThreads - 1) / kSumThreads), static_cast<unsigned>(M < 65535 ? M : 65535)), b(kSumThreads);
   moe_sum_kernel<float><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
       y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
@@ -129,7 +133,7 @@ namespace fmoe {
 // moe_sum of the tiny-batch decode path: y rows are flat slots (t * k + j).
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
-  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M < 65535 ? M : 65535)), b(256);
+  dim3 g(static_cast<unsigned>((K / 4 + kSumThreads - 1) / kSumThreads), static_cast<unsigned>(M < 65535 ? M : 65535)), b(kSumThreads);
   moe_sum_kernel<float><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
                                         static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
@@ -137,7 +141,7 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
 // moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
-  dim3 g(static_cast<unsigned>((K / 4 + 255) / 256), static_cast<unsigned>(M < 65535 ? M : 65535)), b(256);
+  dim3 g(static_cast<unsigned>((K / 4 + kSumThreads - 1) / kSumThreads), static_cast<unsigned>(M < 65535 ? M : 65535)), b(kSumThreads);
   moe_sum_kernel<__bf16><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
                                          nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
