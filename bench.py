@@ -39,6 +39,10 @@ WORKLOADS = {
     "mixtral_bf16_m4096": (4096, 4096, 14336, 8, 2, "bf16", "softmax"),
     "mixtral_bf16_m1": (1, 4096, 14336, 8, 2, "bf16", "softmax"),
     "mixtral_bf16_m16": (16, 4096, 14336, 8, 2, "bf16", "softmax"),
+    "mixtral_bf16_m256": (256, 4096, 14336, 8, 2, "bf16", "softmax"),
+    "tiny_bf16_m64": (64, 128, 256, 8, 2, "bf16", "softmax"),
+    "qwen3_bf16_m1": (1, 2048, 768, 128, 8, "bf16", "softmax_bias"),
+    "qwen3_bf16_m1024": (1024, 2048, 768, 128, 8, "bf16", "softmax_bias"),
     "qwen3_bf16_m8192": (8192, 2048, 768, 128, 8, "bf16", "softmax_bias"),
     "dsv3_fp8_m4096": (4096, 7168, 2048, 256, 8, "fp8", "grouped"),
     "dsv3_fp8_m8192": (8192, 7168, 2048, 256, 8, "fp8", "grouped"),
@@ -60,6 +64,20 @@ WORKLOADS = {
     "mixtral_mxfp4t_m1": (1, 4096, 14336, 8, 2, "mxfp4t", "softmax"),
     "mixtral_mxfp4t_m16": (16, 4096, 14336, 8, 2, "mxfp4t", "softmax"),
 }
+# the reference's own benchmark sweep (benchmark/attri_util.py:45-56):
+# K=1280, N=3072, E=64, top-8, bf16
+for _m in (1, 4, 17, 64, 1024, 2048, 4096):
+    WORKLOADS[f"refsweep_bf16_m{_m}"] = (_m, 1280, 3072, 64, 8, "bf16", "softmax")
+
+# every BASELINE.json point besides the headline, then the reference's sweep
+DEFAULT_SECONDARY = (
+    "dsv3_fp8_m4096,dsv3_fp8_m8192,dsv3_fp8_m1,dsv3_fp8_m128,"
+    "mixtral_w4a16t_m1,mixtral_w4a16t_m4,mixtral_w4a16t_m16,mixtral_w4a16t_m64,"
+    "mixtral_bf16_m1,mixtral_bf16_m16,mixtral_bf16_m256,"
+    "qwen3_bf16_m1,qwen3_bf16_m64,qwen3_bf16_m1024,qwen3_bf16_m8192,tiny_bf16_m64,"
+    + ",".join(f"refsweep_bf16_m{m}" for m in (1, 4, 17, 64, 1024, 2048, 4096)))
+# secondaries that also get a CPU-oracle baseline (the north-star points)
+CPU_SECONDARY = ("dsv3_fp8_m4096", "mixtral_w4a16t_m16")
 
 
 def _wt_codes():
@@ -281,26 +299,80 @@ def stage_times(p, reps=10):
     return acc
 
 
+def host_cores():
+    """Cores this process may run on: the CPU affinity set, capped by a
+    cgroup CPU quota when one is set (a GPU box grants each GPU a share of
+    the host's cores)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, -(-int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def _untile_4bit(t):
+    """One expert of the tiled 4-bit layout [R/16, C/128, 1024] (byte
+    16*(16*g + r) + i of block (b, c) = byte 64*c + 16*g + i of row 16*b + r)
+    back to row-major [R, C/2]."""
+    nb, nc, _ = t.shape
+    return t.view(nb, nc, 4, 16, 16).permute(0, 3, 1, 2, 4).reshape(nb * 16, nc * 64)
+
+
+class _HostExperts:
+    """Per-expert host copies of a device weight tensor, made before the
+    timed region (the oracle then indexes it like the tensor)."""
+
+    def __init__(self, t, experts):
+        self.shape = t.shape
+        self.d = {e: t[e].cpu() for e in experts}
+
+    def __getitem__(self, e):
+        return self.d[e]
+
+
 def cpu_baseline(p, budget_s=10.0):
-    """The CPU oracle (fp32 torch restatement of the reference path) on the
-    first S tokens of the same problem, S sized to about budget_s seconds."""
+    """The CPU oracle (fp32 torch restatement of the reference path, on all
+    cores this process may use) on the first S tokens of the same problem, S
+    sized to about budget_s seconds; the whole problem repeated when it fits.
+    fp8 / int4 weights are dequantized one expert at a time inside the
+    oracle, as a CPU implementation of those formats must (the DeepSeek-V3
+    layer is 45 GB in fp32)."""
     import torch
 
     from oracle import fused_moe_oracle as O
 
-    torch.set_num_threads(min(16, os.cpu_count() or 1))
-    used = sorted(set(p["ti"].flatten().tolist()))
-    if p["wtype"] != "bf16":
-        return None
-    w13 = p["w13"].cpu()
-    w2 = p["w2"].cpu()
+    torch.set_num_threads(host_cores())
     x = p["x"].cpu()
     tw = p["tw"].cpu()
     ti = p["ti"].cpu()
+    kw = p["kw"]
+    if p["wtype"] == "bf16":
+        w13, w2 = p["w13"].cpu(), p["w2"].cpu()
+        fn = lambda S: O.fused_experts(x[:S], w13, w2, tw[:S], ti[:S])  # noqa: E731
+    else:
+        hit = sorted(set(ti.flatten().tolist()))
+        hx = {n: _HostExperts(t, hit) for n, t in
+              (("q1", p["w13"]), ("q2", p["w2"]), ("s1", kw["w1_scale"]), ("s2", kw["w2_scale"]))}
+        if p["wtype"] == "fp8":
+            fn = lambda S: O.fused_experts_fp8(x[:S], hx["q1"], hx["s1"], hx["q2"], hx["s2"],  # noqa: E731
+                                               tw[:S], ti[:S])
+        elif p["wtype"] in ("int4", "int4t"):
+            if p["wtype"] == "int4t":  # the oracle reads the row-major packing
+                hx["q1"].d = {e: _untile_4bit(v) for e, v in hx["q1"].d.items()}
+                hx["q2"].d = {e: _untile_4bit(v) for e, v in hx["q2"].d.items()}
+            z1, z2 = _HostExperts(kw["w1_zp"], hit), _HostExperts(kw["w2_zp"], hit)
+            fn = lambda S: O.fused_experts_w4a16(x[:S], hx["q1"], hx["s1"], z1, hx["q2"],  # noqa: E731
+                                                 hx["s2"], z2, tw[:S], ti[:S])
+        else:
+            return None
 
     def run(S):
         t0 = time.perf_counter()
-        O.fused_experts(x[:S], w13, w2, tw[:S], ti[:S])
+        fn(S)
         return time.perf_counter() - t0
 
     S = min(p["M"], 64)
@@ -313,13 +385,16 @@ def cpu_baseline(p, budget_s=10.0):
     while sum(times) < budget_s:
         times.append(run(S))
     t = sum(times) / len(times)
-    del used
     f = 6.0 * S * p["k"] * p["K"] * p["N"]
-    return {"value": round(f / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"first {S} of {p['M']} tokens x {len(times)} runs, oracle/fused_moe_oracle.py "
-                      f"fused_experts (fp32 torch on CPU, includes per-expert weight upcast), "
-                      f"{sum(times):.1f} s in total, mean {t:.2f} s per run"}
+    res = {"value": round(f / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+           "kind": "port",
+           "sample": f"first {S} of {p['M']} tokens x {len(times)} runs, oracle/fused_moe_oracle.py "
+                     f"({'fused_experts' if p['wtype'] == 'bf16' else 'fused_experts_' + p['wtype'].rstrip('t')}"
+                     f", fp32 torch on CPU, per-expert weight upcast / dequantization included), "
+                     f"{sum(times):.1f} s in total, mean {t:.3f} s per run"}
+    if S == p["M"]:
+        res["ms"] = round(t * 1e3, 2)
+    return res
 
 
 def _load_traffic(name):
@@ -450,10 +525,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="mixtral_bf16_m4096", choices=sorted(WORKLOADS))
-    ap.add_argument("--secondary", default="dsv3_fp8_m4096,mixtral_w4a16t_m1,mixtral_w4a16t_m4,"
-                                           "mixtral_w4a16t_m16,mixtral_w4a16t_m64,mixtral_w4a16_m1,"
-                                           "mixtral_w4a16_m16,dsv3_fp8_m1,dsv3_fp8_m128,qwen3_bf16_m64,"
-                                           "qwen3_bf16_m8192",
+    ap.add_argument("--secondary", default=DEFAULT_SECONDARY,
                     help="comma list of extra workloads reported in 'secondary' ('' for none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calib", action="store_true",
@@ -501,7 +573,10 @@ def main():
     sec = []
     for name in [s for s in args.secondary.split(",") if s and s != args.workload]:
         r = measure(name, max(5, args.steps // 2), args.warmup)
-        sec.append(secondary_entry(r))
+        e = secondary_entry(r)
+        if name in CPU_SECONDARY and not args.no_cpu:
+            e["cpu_baseline"] = cpu_baseline(r["p"])
+        sec.append(e)
         del r
         torch.cuda.empty_cache()
     line["secondary"] = sec
