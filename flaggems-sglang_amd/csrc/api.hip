@@ -372,11 +372,17 @@ FusedLayout layout(const fmoe_fused_args* a) {
 // Tiny decode batches: every tile holds at most 16 slots and the whole
 // routing fits one workgroup's LDS, so the GEMM workgroups compute their own
 // tile from the top-k ids (no align launch); rows are flat slots t * k + j.
-// bf16 / fp8 only: for int4 the separate align launch measured faster (its
-// GEMMs are short enough that the in-workgroup routing latency shows).
+// bf16 / fp8 up to 16 tokens; int4 only for a single token (Mixtral shape:
+// M = 1 60.8 -> 58.5 us, M = 4 / 16 slower than with the align launch, whose
+// tiles let the GEMM workgroups start without the routing latency); MXFP4
+// never (measured slower).
 bool tiny_decode(const fmoe_fused_args* a, const FusedLayout& L) {
-  return L.bm == kDecodeBM && !decode_only(a->wtype) && a->M <= 16 && a->M * a->top_k <= 512 &&
-         a->E <= 1024 && !a->expert_map;
+#ifndef FMOE_TINY_INT4_MAX_M
+#define FMOE_TINY_INT4_MAX_M 1
+#endif
+  const int64_t max_m = is_int4(a->wtype) ? FMOE_TINY_INT4_MAX_M : (is_mx(a->wtype) ? 0 : 16);
+  return L.bm == kDecodeBM && a->M <= max_m && a->M * a->top_k <= 512 && a->E <= 1024 &&
+         !a->expert_map;
 }
 
 int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStream_t s) {

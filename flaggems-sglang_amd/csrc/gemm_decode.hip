@@ -668,7 +668,7 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   do {                                                                                                \
     constexpr int RB_ = decode_row_blocks(WT_);                                                       \
     const dim3 b_(decode::kThreads * RB_);                                                            \
-    if (p.tiny_ids && WT_ != WType::kInt4 && WT_ != WType::kMxfp4)                                    \
+    if (p.tiny_ids && WT_ != WType::kMxfp4)                                                          \
       decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_, true), ACT_, true, RB_><<<g, b_, 0, s>>>(p); \
     else                                                                                              \
       decode::gemm_decode_kernel<WT_, MODE_, decode::pipe_depth(WT_, MODE_, false), ACT_, false, RB_><<<g, b_, 0, s>>>(p); \
