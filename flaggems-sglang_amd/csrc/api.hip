@@ -24,6 +24,10 @@ constexpr int kDecodeBN = 64;
 constexpr int kDecodeTargetWgs = 1024;
 constexpr int kPrefillBN = 256;
 constexpr int kPrefillTargetWgs = 6 * 256;
+// at or above this many output tiles (2.5 waves of one workgroup per CU) the
+// last wave's tail costs less than writing and re-reading fp32 split planes
+// (reference sweep K=1280 N=3072 E=64 M=4096: 1.31 -> 1.19 ms unsplit)
+constexpr int kPrefillNoSplitWgs = 640;
 
 size_t al(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -102,12 +106,14 @@ extern "C" int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_rou
   (void)path;
   if (!r) return 1;
   if (!is_decode(r)) {
-    // Prefill GEMM2 has few output tiles (K / 256 per M-tile): split the
-    // reduction dim until the grid covers >= 6 waves of one workgroup per CU,
-    // so the last wave's tail stays small.  Partials are summed by moe_sum.
+    // Prefill GEMM2 has few output tiles (K / 256 per M-tile): below
+    // kPrefillNoSplitWgs tiles, split the reduction dim until the grid covers
+    // >= 6 waves of one workgroup per CU, so the last wave's tail stays small.
+    // Partials are summed by moe_sum.
     const int64_t slots = r->n_tokens * r->top_k;
     const int64_t tiles = (slots + r->block_m - 1) / r->block_m;
     const int64_t wgs = tiles * ((K + kPrefillBN - 1) / kPrefillBN);
+    if (wgs >= kPrefillNoSplitWgs) return 1;
     const int64_t stage_elems = wtype == FMOE_W_BF16 ? 32 : 128;
     int64_t sp = (kPrefillTargetWgs + wgs - 1) / (wgs > 0 ? wgs : 1);
     const int64_t max_sp = N / stage_elems / 16 > 1 ? N / stage_elems / 16 : 1;  // >= 16 stages each
