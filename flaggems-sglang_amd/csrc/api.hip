@@ -21,7 +21,10 @@ namespace {
 
 constexpr int kDecodeBM = 16;
 constexpr int kDecodeBN = 64;
-constexpr int kDecodeTargetWgs = 1024;
+#ifndef FMOE_DECODE_TARGET_WGS
+#define FMOE_DECODE_TARGET_WGS 1024
+#endif
+constexpr int kDecodeTargetWgs = FMOE_DECODE_TARGET_WGS;
 constexpr int kPrefillBN = 256;
 constexpr int kPrefillTargetWgs = 6 * 256;
 // at or above this many output tiles (2.5 waves of one workgroup per CU) the
