@@ -446,7 +446,7 @@ extern "C" int fmoe_align_ex(const int32_t* topk_ids, const float* topk_weights,
   if (M < 0 || k < 1 || k > 32 || E < 1 || E > kMaxExperts)
     return fail(FMOE_ERR_INVALID, "align: need 1 <= k <= 32, 1 <= E <= %d (M=%lld k=%d E=%d)",
                 kMaxExperts, static_cast<long long>(M), k, E);
-  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256)
+  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128 && block_m != 160 && block_m != 256)
     return fail(FMOE_ERR_UNSUPPORTED, "align: block_m=%d is not supported", block_m);
   if (M * k > (int64_t(1) << 31) - 1 || M * k / block_m + E >= (1 << 15))
     return fail(FMOE_ERR_UNSUPPORTED, "align: %lld slots is not supported", static_cast<long long>(M * k));
@@ -496,7 +496,7 @@ extern "C" int fmoe_expt_data(const int32_t* hist, int E, int64_t n_slots, int b
                               int32_t* n_tiles, void* stream) {
   if (E < 1 || E > kMaxExperts || n_slots < 0)
     return fail(FMOE_ERR_INVALID, "expt_data: need 1 <= E <= %d", kMaxExperts);
-  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128 && block_m != 256)
+  if (block_m != 16 && block_m != 32 && block_m != 64 && block_m != 128 && block_m != 160 && block_m != 256)
     return fail(FMOE_ERR_UNSUPPORTED, "expt_data: block_m=%d is not supported", block_m);
   if (!hist || !offs_raw || !offs_pad || !tile_map || !n_tiles)
     return fail(FMOE_ERR_INVALID, "expt_data: null pointer");

@@ -1,4 +1,5 @@
 // C-ABI entry points of the GEMM stages and the whole fused path.
+#include <cmath>
 #include <mutex>
 
 #include "gemm.hpp"
@@ -56,7 +57,8 @@ int check_routing(const fmoe_routing* r, const char* who) {
     return fail(FMOE_ERR_INVALID, "%s: routing pointer is null", who);
   if (r->n_tokens < 0 || r->top_k < 1 || r->n_experts < 1 || r->max_tiles < 0)
     return fail(FMOE_ERR_INVALID, "%s: bad routing sizes", who);
-  if (r->block_m != 16 && r->block_m != 64 && r->block_m != 128 && r->block_m != 256)
+  if (r->block_m != 16 && r->block_m != 64 && r->block_m != 128 && r->block_m != 160 &&
+      r->block_m != 256)
     return fail(FMOE_ERR_UNSUPPORTED, "%s: block_m=%d is not supported", who, r->block_m);
   if (r->block_m != 16 && !r->offs_pad)
     return fail(FMOE_ERR_INVALID, "%s: prefill routing needs offs_pad", who);
@@ -88,7 +90,8 @@ GemmParams base_params(const fmoe_routing* r) {
 // Tile height for the fused path: 16 = decode kernels, else the prefill tile,
 // from the mean slots per expert (measured on the BASELINE shapes): bf16
 // 256-row tiles once experts average >= 256 slots, 128-row tiles from 40
-// (a half-empty 128-row tile still beats a 64-row one), else 64.
+// (a half-empty 128-row tile still beats a 64-row one), else 64; fp8 160-row
+// tiles as below.
 int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
   const int64_t slots = M * k;
   const int64_t active = slots < E ? slots : E;
@@ -96,8 +99,20 @@ int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
   if (path != 1 && slots <= kDecodeBM * (active > 0 ? active : 1)) return kDecodeBM;
   const int64_t mean = slots / E;
   if (wtype == FMOE_W_BF16 && mean >= 256) return 256;
-  return mean >= 40 ? 128 : 64;
+  if (mean < 40) return 64;
+  if (wtype == FMOE_W_FP8) {
+    // fp8: 160-row tiles where they need fewer M-tiles per expert than
+    // 128-row ones at the mean + 2 sd of a uniform routing's per-expert load
+    // (each M-tile streams the expert's whole weight panel again)
+    const double q = static_cast<double>(mean) + 2.0 * std::sqrt(static_cast<double>(mean));
+    if (std::ceil(q / 160.0) < std::ceil(q / 128.0)) return 160;
+  }
+  return 128;
 }
+
+// The 160-row fp8 tile stages the weight scales of at most 64 reduction
+// blocks (K, N <= 8192); larger layers take 128-row tiles.
+int fit_block_m(int bm, int64_t K, int64_t N) { return bm == 160 && (K > 8192 || N > 8192) ? 128 : bm; }
 
 }  // namespace
 
@@ -336,7 +351,7 @@ int check_fused(const fmoe_fused_args* a) {
 FusedLayout layout(const fmoe_fused_args* a) {
   FusedLayout L{};
   const int64_t slots = a->M * a->top_k;
-  L.bm = choose_block_m(a->wtype, a->M, a->top_k, a->E, a->path);
+  L.bm = fit_block_m(choose_block_m(a->wtype, a->M, a->top_k, a->E, a->path), a->K, a->N);
   L.max_tiles = fmoe_max_tiles(slots, a->E);
   fmoe_routing r{};
   r.n_tokens = a->M;

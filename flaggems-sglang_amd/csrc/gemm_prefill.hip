@@ -40,7 +40,7 @@ namespace fmoe {
 namespace prefill {
 
 constexpr int kUnit = 1024;       // one DMA wave-instruction: 64 lanes x 16 B
-constexpr int kMaxKStages = 128;  // fp8: reduction dims up to 16384
+constexpr int kMaxKStages = 128;  // fp8: reduction dims up to 16384 (64 stages when LDS is short)
 constexpr int kGroupTiles = 32;   // tiles per rasterization window (~ one XCD's CUs)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -57,15 +57,25 @@ struct Cfg {
   static constexpr int UPB = SB / 64;                       // units per 16-row block
   static_assert(SB == 64 || SB == 128, "stage width");
   static constexpr int A_UNITS = (BM / 16) * UPB, B_UNITS = (BN / 16) * UPB;
-  static constexpr int UPW = (A_UNITS + B_UNITS) / NW;      // DMA per wave per stage
-  static constexpr int A_UPW = A_UNITS / NW;
-  static constexpr int STAGE = (A_UNITS + B_UNITS) * kUnit;
-  static constexpr int SA_WAVES = FP8 ? BM / 64 : 0;        // waves that DMA a-scales
-  static_assert((A_UNITS % NW) == 0 && (B_UNITS % NW) == 0, "units per wave");
+  // unit u of a stage is DMAed by wave u % NW: waves below REM (or all of
+  // them when REM == 0) issue UPW units per stage, the others UPW - 1
+  static constexpr int UNITS = A_UNITS + B_UNITS;
+  static constexpr int UPW = (UNITS + NW - 1) / NW;
+  static constexpr int REM = UNITS % NW;
+  static constexpr int STAGE = UNITS * kUnit;
+  // waves that DMA the activation scales (64 rows each): the last SA_WAVES
+  // waves, which carry the fewer units when the split is uneven
+  static constexpr int SA_WAVES = FP8 ? (BM + 63) / 64 : 0;
+  static constexpr int SA_FIRST = NW - SA_WAVES;
+  // fp8 weight-scale stages held in LDS (the reduction dim is at most 128 KST)
+  static constexpr int KST =
+      NBUF * STAGE + NBUF * BM * 4 + WAVES_N * 2 * kMaxKStages * 4 <= 160 * 1024 ? kMaxKStages : 64;
+  static_assert(BM % 16 == 0 && (A_UNITS % 2) == 0, "16-row blocks");
+  static_assert(REM == 0 || REM <= SA_FIRST || !FP8, "a-scale waves carry the fewer units");
   static_assert(!FP8 || SB == 128, "fp8 stages hold one 128-wide scale block");
   static_assert(MODE != Mode::kGemm1Silu || NI % 2 == 0, "gate/up pairing needs even NI");
   static_assert(NBUF >= 2 && NBUF <= 4, "ring depth");
-  static_assert(NBUF * STAGE + NBUF * BM * 4 + WAVES_N * 2 * kMaxKStages * 4 <= 160 * 1024, "LDS budget");
+  static_assert(NBUF * STAGE + NBUF * BM * 4 + WAVES_N * 2 * KST * 4 <= 160 * 1024, "LDS budget");
   static_assert(SA_WAVES <= NW, "a-scale waves");
 };
 
@@ -73,6 +83,14 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   __builtin_amdgcn_s_waitcnt((N & 0xf) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
+// wait until at most `newer` stages (P loads each) of this wave are in flight
+template <int P>
+__device__ __forceinline__ void wait_ring(int newer) {
+  if (newer >= 2) wait_vmcnt<2 * P>();
+  else if (newer == 1) wait_vmcnt<P>();
+  else wait_vmcnt<0>();
 }
 
 __device__ __forceinline__ void barrier_nofence() { asm volatile("s_barrier" ::: "memory"); }
@@ -203,7 +221,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   constexpr Mode MODE = C::MODE;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NBUF][C::STAGE];
   __shared__ __attribute__((aligned(256))) float sa_lds[NBUF][FP8 ? BM : 1];
-  __shared__ float sb_lds[C::WAVES_N][2][FP8 ? kMaxKStages : 1];
+  __shared__ float sb_lds[C::WAVES_N][2][FP8 ? C::KST : 1];
 
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -251,9 +269,10 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * kbytes;
   const uint8_t* src[C::UPW];
   int loff[C::UPW];
+  const bool full_wave = C::REM == 0 || wid < C::REM;  // issues UPW units (else UPW - 1)
 #pragma unroll
   for (int i = 0; i < C::UPW; ++i) {
-    const int u = NW * i + wid;
+    const int u = min(NW * i + wid, C::UNITS - 1);
     const int b = u / UPB;
     int lr, coff;  // row within the 16-row block, byte offset in the row slice
     if constexpr (SB == 64) {
@@ -265,7 +284,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       coff = ((lane & 7) ^ ru) * 16;
     }
     loff[i] = u * kUnit;
-    if (i < C::A_UPW) {
+    if (u < C::A_UNITS) {
       src[i] = p.A + a_src_row(b * 16 + lr) * kbytes + static_cast<int64_t>(k0) * SB + coff;
     } else {
       const int r = (b - BM / 16) * 16 + lr;  // row of the B tile
@@ -281,9 +300,13 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       src[i] = Be + brow * kbytes + static_cast<int64_t>(k0) * SB + coff;
     }
   }
-  // fp8: waves 0 .. BM/64-1 DMA the activation scales of rows 64 wid + lane
+  // fp8: waves SA_FIRST + j DMA the activation scales of rows 64 j + lane
+  // (lanes past BM stay idle)
+  const int sa_j = wid - C::SA_FIRST;
+  const bool sa_wave = FP8 && sa_j >= 0;
+  const bool sa_lane = sa_wave && 64 * sa_j + lane < BM;
   const float* sa_src = nullptr;
-  if (FP8 && wid < C::SA_WAVES) sa_src = p.a_scale + a_src_row(64 * wid + lane) * ksb + k0;
+  if (sa_wave) sa_src = p.a_scale + a_src_row(min(64 * sa_j + lane, BM - 1)) * ksb + k0;
   // fp8 weight scales of the whole k range, staged once in LDS
   if (FP8) {
     const int64_t nrb = p.Nout / 128;
@@ -313,8 +336,15 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     uint8_t* st = lds[kt % NBUF];
     const int64_t off = static_cast<int64_t>(kt) * SB;
 #pragma unroll
-    for (int i = 0; i < C::UPW; ++i) dma16(src[i] + off, st + loff[i]);
-    if (FP8 && wid < C::SA_WAVES) dma4(sa_src + kt, &sa_lds[kt % NBUF][64 * wid]);
+    for (int i = 0; i < C::UPW; ++i)
+      if (i + 1 < C::UPW || full_wave) dma16(src[i] + off, st + loff[i]);
+    if (sa_wave) {
+      if (64 * (sa_j + 1) <= BM) {
+        dma4(sa_src + kt, &sa_lds[kt % NBUF][64 * sa_j]);
+      } else if (sa_lane) {  // partial last 64-row group: masked lanes write nothing
+        dma4(sa_src + kt, &sa_lds[kt % NBUF][64 * sa_j]);
+      }
+    }
   };
 
   f32x4_t acc[MI][NI];
@@ -382,16 +412,14 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
   for (int s = 0; s < NBUF - 1; ++s)
     if (s < nk) issue(s);
-  constexpr int kPer = C::UPW;  // DMA instructions per stage for this wave
-  constexpr int kPerSa = C::UPW + (FP8 ? 1 : 0);
-  const bool sa_wave = FP8 && wid < C::SA_WAVES;
+  // DMA instructions per stage for this wave: UPW or UPW - 1 operand units,
+  // plus one a-scale load
+  const int per = (full_wave ? C::UPW : C::UPW - 1) + (sa_wave ? 1 : 0);
   for (int kt = 0; kt < nk; ++kt) {
     const int newer = min(NBUF - 2, nk - 1 - kt);
-    if (sa_wave) {
-      if (newer >= 2) wait_vmcnt<2 * kPerSa>(); else if (newer == 1) wait_vmcnt<kPerSa>(); else wait_vmcnt<0>();
-    } else {
-      if (newer >= 2) wait_vmcnt<2 * kPer>(); else if (newer == 1) wait_vmcnt<kPer>(); else wait_vmcnt<0>();
-    }
+    if (per == C::UPW + 1) wait_ring<C::UPW + 1>(newer);
+    else if (per == C::UPW) wait_ring<C::UPW>(newer);
+    else wait_ring<(C::UPW > 1 ? C::UPW - 1 : 1)>(newer);
     barrier_nofence();
     if (kt + NBUF - 1 < nk) issue(kt + NBUF - 1);
     compute(kt);
@@ -532,7 +560,7 @@ int launch(const GemmParams& p0, hipStream_t s) {
   const int64_t grid = static_cast<int64_t>(p.max_tiles) * p.n_ntiles * p.splits;
   if (grid <= 0) return FMOE_OK;
   if (grid > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill grid too large");
-  if (C::FP8 && p.Kred / 128 > kMaxKStages)
+  if (C::FP8 && p.Kred / 128 > C::KST)
     return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill fp8: reduction dim %lld is not supported",
                            static_cast<long long>(p.Kred));
   if (p.tile_lut) {
@@ -555,7 +583,8 @@ int launch(const GemmParams& p0, hipStream_t s) {
 //   bf16: BM 256 -> 256x256, 4x2 waves, 128-byte stages, 2-deep ring
 //         BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM  64 ->  64x256, 1x4 waves, 64-byte stages, 4-deep ring
-//   fp8 : BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
+//   fp8 : BM 160 -> 160x256, 2x4 waves, 128-byte stages, 3-deep ring (K <= 8192)
+//         BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM  64 ->  64x256, 1x8 waves, 128-byte stages, 3-deep ring
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s) {
   using namespace prefill;
@@ -568,6 +597,7 @@ int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t
     if (bm == 128) return L(128, 256, 2, 4, 128, 3, false);
     if (bm == 64) return L(64, 256, 1, 4, 64, 4, false);
   } else {
+    if (bm == 160) return L(160, 256, 2, 4, 128, 3, true);
     if (bm == 128) return L(128, 256, 2, 4, 128, 3, true);
     if (bm == 64) return L(64, 256, 1, 8, 128, 3, true);
   }

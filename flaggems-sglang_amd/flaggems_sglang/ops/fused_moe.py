@@ -177,6 +177,14 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: i
     return a.sorted_token_ids, a.expert_ids, a.num_tokens_post_padded
 
 
+def _block_m(wtype: int, M: int, k: int, E: int, path: int, K: int, N: int) -> int:
+    """The fused path's tile height (fmoe_choose_block_m), with 160-row fp8
+    tiles replaced by 128-row ones when K or N exceeds 8192 (the 160-row
+    kernel stages the weight scales of at most 64 reduction blocks)."""
+    bm = lib().fmoe_choose_block_m(wtype, M, k, E, path)
+    return 128 if bm == 160 and max(K, N) > 8192 else bm
+
+
 def _standard_topk_to_triton_kernels(topk_weights, topk_ids, n_expts_tot, block_m: Optional[int] = None):
     """Convert standard top-k output to routing data (ops/fused_moe.py:103-130).
 
@@ -429,7 +437,7 @@ def triton_kernel_fused_experts(
     w2t = _as_sglang_layout(w2)
     s13 = None if w1_scale is None else _as_sglang_layout(w1_scale)
     s2 = None if w2_scale is None else _as_sglang_layout(w2_scale)
-    bm = lib().fmoe_choose_block_m(wtype, M, k, E, 0)
+    bm = _block_m(wtype, M, k, E, 0, x.shape[1], w2.shape[1])
     offs_raw, offs_pad, tile_map, n_tiles = _expt_data_for(routing_data, M * k, bm)
     topk_indx = gather_indx.src_indx.to(torch.int32).contiguous()
     gate_indx = gather_indx.dst_indx.to(torch.int32).contiguous()
@@ -619,7 +627,7 @@ def fused_experts(
         # SGLang's no_combine contract: [M, k, K] with slot (t, j) = the
         # expert topk_ids[t, j] (routed_scaling_factor not applied, as in the
         # reference hook, ops/fused_moe.py:399-404)
-        a = _align(topk_weights, topk_ids, E, lib().fmoe_choose_block_m(wtype, M, k, E, path), False,
+        a = _align(topk_weights, topk_ids, E, _block_m(wtype, M, k, E, path, K, N), False,
                    expert_map=emap)
         return _run_stages(x, w1, w2, wtype, w1_scale, w2_scale, w1_zp, w2_zp, M, k, E,
                            a.topk_indx, a.gate_indx, a.gate_scal, a.offs_raw, a.offs_pad, a.tile_map,

@@ -47,7 +47,12 @@ def test_host_queries():
     assert L.fmoe_choose_block_m(_lib.W_BF16, 4096, 2, 8, 0) == 256
     assert L.fmoe_choose_block_m(_lib.W_BF16, 1024, 8, 128, 0) == 128
     assert L.fmoe_choose_block_m(_lib.W_BF16, 400, 8, 128, 0) == 64
-    assert L.fmoe_choose_block_m(_lib.W_FP8, 4096, 8, 256, 0) == 128
+    # fp8: 160-row tiles where the mean + 2 sd load per expert needs fewer of
+    # them than of 128-row tiles (DSV3 M=4096: 128 +- 11 slots per expert)
+    assert L.fmoe_choose_block_m(_lib.W_FP8, 4096, 8, 256, 0) == 160
+    assert L.fmoe_choose_block_m(_lib.W_FP8, 8192, 8, 256, 0) == 160
+    assert L.fmoe_choose_block_m(_lib.W_FP8, 3072, 8, 256, 0) == 128
+    assert L.fmoe_choose_block_m(_lib.W_FP8, 6400, 8, 256, 0) == 128
 
 
 def test_argument_errors_map_to_reference_convention():
