@@ -45,11 +45,30 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
   }
 }
 
-// out[t, c] = bf16(scale * sum_j sum_p y[p][gate_indx[t*k+j], c]); j then p
-// in ascending order.  One thread = 4 columns (16-byte loads).
-// out[t] = bf16(scale * sum over the token's k slots, then over the split
-// planes, in that fixed order).
+// out[t, c] = bf16(scale * sum_j sum_p y[p][gate_indx[t*k+j], c]): the
+// token's k slots in ascending j, each slot's split planes in ascending p,
+// one running fp32 sum per column in exactly that order (deterministic).
+// One thread = 4 columns (16-byte loads); the (j, p) terms are fetched
+// kBatch at a time so their loads are in flight together.
 constexpr int kSumThreads = 256;
+constexpr int kBatch = 8;
+
+template <typename YT>
+__device__ __forceinline__ void load4(const YT* src, float (&v)[4]) {
+  if constexpr (sizeof(YT) == 4) {
+    const float4 f = *reinterpret_cast<const float4*>(src);
+    v[0] = f.x;
+    v[1] = f.y;
+    v[2] = f.z;
+    v[3] = f.w;
+  } else {  // bf16 rows
+    const uint2 w = *reinterpret_cast<const uint2*>(src);
+    v[0] = __uint_as_float(w.x << 16);
+    v[1] = __uint_as_float(w.x & 0xffff0000u);
+    v[2] = __uint_as_float(w.y << 16);
+    v[3] = __uint_as_float(w.y & 0xffff0000u);
+  }
+}
 
 template <typename YT>
 __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restrict__ y, int splits,
@@ -60,36 +79,55 @@ __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restri
                                                               uint16_t* __restrict__ out) {
   const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
   if (c >= K) return;
+  const int n_terms = k * splits;
   // tokens t = blockIdx.y, blockIdx.y + gridDim.y, ... (grid y is capped at 65535)
   for (int64_t t = blockIdx.y; t < n_tok; t += gridDim.y) {
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    for (int j = 0; j < k; ++j) {
-      // tiny-batch path (gate_indx null): slot = flat index, dropped when its
-      // expert id is out of range
-      const int s = gate_indx ? gate_indx[t * k + j]
-                              : (ids[t * k + j] >= 0 && ids[t * k + j] < n_experts ? static_cast<int>(t * k + j) : -1);
-      if (s < 0) continue;  // slot routed to no expert
-      for (int p = 0; p < splits; ++p) {
-        const YT* src = y + p * split_stride + static_cast<int64_t>(s) * K + c;
-        if constexpr (sizeof(YT) == 4) {
-          const float4 v = *reinterpret_cast<const float4*>(src);
-          a0 += v.x;
-          a1 += v.y;
-          a2 += v.z;
-          a3 += v.w;
-        } else {  // bf16 rows
-          const uint2 v = *reinterpret_cast<const uint2*>(src);
-          a0 += __uint_as_float(v.x << 16);
-          a1 += __uint_as_float(v.x & 0xffff0000u);
-          a2 += __uint_as_float(v.y << 16);
-          a3 += __uint_as_float(v.y & 0xffff0000u);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int j = 0, p = 0;  // (slot, plane) of the batch's first term
+    for (int b = 0; b < n_terms; b += kBatch) {
+      float v[kBatch][4];
+      bool live[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        live[u] = false;
+        if (b + u < n_terms) {
+          // tiny-batch path (gate_indx null): slot = flat index, dropped when
+          // its expert id is out of range; else a negative slot is dropped
+          const int64_t f = t * k + j;
+          const int sl = gate_indx ? gate_indx[f]
+                                   : (ids[f] >= 0 && ids[f] < n_experts ? static_cast<int>(f) : -1);
+          if (sl >= 0) {
+            load4(y + p * split_stride + static_cast<int64_t>(sl) * K + c, v[u]);
+            live[u] = true;
+          }
+          if (++p == splits) {
+            p = 0;
+            ++j;
+          }
         }
       }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (live[u]) {
+          acc[0] += v[u][0];
+          acc[1] += v[u][1];
+          acc[2] += v[u][2];
+          acc[3] += v[u][3];
+        }
     }
-    const uint32_t w0 = f32_to_bf16(a0 * scale) | (static_cast<uint32_t>(f32_to_bf16(a1 * scale)) << 16);
-    const uint32_t w1 = f32_to_bf16(a2 * scale) | (static_cast<uint32_t>(f32_to_bf16(a3 * scale)) << 16);
+    const uint32_t w0 = f32_to_bf16(acc[0] * scale) | (static_cast<uint32_t>(f32_to_bf16(acc[1] * scale)) << 16);
+    const uint32_t w1 = f32_to_bf16(acc[2] * scale) | (static_cast<uint32_t>(f32_to_bf16(acc[3] * scale)) << 16);
     *reinterpret_cast<uint2*>(out + t * K + c) = make_uint2(w0, w1);
   }
+}
+
+// Small calls (decode) use 64-thread blocks, so their few workgroups spread
+// over more CUs (each CU keeps only so many loads in flight).
+inline void sum_launch_dims(int64_t K, int64_t M, dim3& g, dim3& b) {
+  const int64_t vecs = K / 4;
+  const int threads = vecs * M < 64 * 1024 ? 64 : kSumThreads;
+  g = dim3(static_cast<unsigned>((vecs + threads - 1) / threads), static_cast<unsigned>(M < 65535 ? M : 65535));
+  b = dim3(static_cast<unsigned>(threads));
 }
 
 }  // namespace fmoe
@@ -123,7 +161,8 @@ extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx
     return fail(FMOE_ERR_INVALID, "moe_sum: need K %% 4 == 0, k >= 1, splits >= 1");
   if (M == 0) return FMOE_OK;
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
-  dim3 g(static_cast<unsigned>((K / 4 + kSumThreads - 1) / kSumThreads), static_cast<unsigned>(M < 65535 ? M : 65535)), b(kSumThreads);
+  dim3 g, b;
+  sum_launch_dims(K, M, g, b);
   moe_sum_kernel<float><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
       y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
@@ -133,7 +172,8 @@ namespace fmoe {
 // moe_sum of the tiny-batch decode path: y rows are flat slots (t * k + j).
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
-  dim3 g(static_cast<unsigned>((K / 4 + kSumThreads - 1) / kSumThreads), static_cast<unsigned>(M < 65535 ? M : 65535)), b(kSumThreads);
+  dim3 g, b;
+  sum_launch_dims(K, M, g, b);
   moe_sum_kernel<float><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
                                         static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
@@ -141,7 +181,8 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
 // moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
-  dim3 g(static_cast<unsigned>((K / 4 + kSumThreads - 1) / kSumThreads), static_cast<unsigned>(M < 65535 ? M : 65535)), b(kSumThreads);
+  dim3 g, b;
+  sum_launch_dims(K, M, g, b);
   moe_sum_kernel<__bf16><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
                                          nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
