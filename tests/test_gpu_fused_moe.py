@@ -154,6 +154,32 @@ def test_dsv3_fp8(M):
     _close(out, ref, 5e-2)
 
 
+@pytest.mark.parametrize("K,N", [(7168, 256), (8448, 256), (256, 8448)])
+def test_fp8_tile_height_choice(K, N):
+    """fp8 prefill at ~128 slots per expert picks 160-row tiles (one M-tile
+    for experts of up to 160 slots); with K or N above 8192 the fused path
+    and the stage path (triton_kernel_fused_experts) fall back to 128-row
+    tiles.  Both against the oracle; uneven expert loads from the routing."""
+    M, E, k = 256, 8, 4
+    from flaggems_sglang import _lib as LB
+    assert LB.lib().fmoe_choose_block_m(LB.W_FP8, M, k, E, 0) == 160
+    assert F._block_m(LB.W_FP8, M, k, E, 0, K, N) == (160 if max(K, N) <= 8192 else 128)
+    d = O.make_inputs(M, K, N, E, k, wscale=0.02)
+    q1, s1 = Q.quantize_fp8_block(d["w13"].to(DEV))
+    q2, s2 = Q.quantize_fp8_block(d["w2"].to(DEV))
+    tw, ti = d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    ref = O.fused_experts_fp8(d["x"], q1.cpu(), s1.cpu(), q2.cpu(), s2.cpu(), d["topk_weights"],
+                              d["topk_ids"])
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), q1, q2, tw, ti, use_fp8_w8a8=True, w1_scale=s1,
+                                        w2_scale=s2, block_shape=[128, 128])
+    _close(out, ref, 5e-2)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw, ti, E)
+    out2 = flaggems_sglang.triton_kernel_fused_experts(
+        d["x"].to(DEV), q1.transpose(1, 2), q2.transpose(1, 2), rd, gi, si, use_fp8_w8a8=True,
+        w1_scale=s1.transpose(1, 2), w2_scale=s2.transpose(1, 2), block_shape=[128, 128])
+    _close(out2, ref, 5e-2)
+
+
 @pytest.mark.parametrize("M", [1, 4, 16, 64])
 def test_mixtral_w4a16(M):
     K, N, E, k = 4096, 14336, 8, 2
