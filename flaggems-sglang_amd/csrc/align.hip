@@ -127,23 +127,42 @@ __device__ void phase_scan(const AlignParams& p, const int32_t* hist_in, int* of
   int hv[PER], tv[PER];
   int hsum = 0, tsum = 0;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    int e = tid * PER + i;
-    int run = 0;
-    if (e < p.E) {
-      if (hist_in) {
-        run = hist_in[e];
-      } else {
-        for (int c = 0; c < p.n_chunks; ++c) {
-          int64_t ix = static_cast<int64_t>(c) * p.E + e;
-          int v = p.chunk_hist[ix];
-          p.chunk_base[ix] = run;
-          run += v;
-        }
-      }
+  for (int i = 0; i < PER; ++i) hv[i] = 0;
+  if (hist_in) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid * PER + i;
+      if (e < p.E) hv[i] = hist_in[e];
     }
-    hv[i] = run;
-    tv[i] = (run + p.bm - 1) / p.bm;
+  } else {
+    // per expert, exclusive prefix over the chunks: the loads of kBatch
+    // chunks x PER experts are issued together (the chunk_base stores
+    // cannot alias them), instead of one dependent round trip per chunk
+    constexpr int kBatch = 8;
+    const int32_t* __restrict__ ch = p.chunk_hist;
+    int32_t* __restrict__ cb = p.chunk_base;
+    for (int c0 = 0; c0 < p.n_chunks; c0 += kBatch) {
+      int v[kBatch][PER];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int e = tid * PER + i;
+          v[b][i] = (c0 + b < p.n_chunks && e < p.E) ? ch[static_cast<int64_t>(c0 + b) * p.E + e] : 0;
+        }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int e = tid * PER + i;
+          if (c0 + b < p.n_chunks && e < p.E) cb[static_cast<int64_t>(c0 + b) * p.E + e] = hv[i];
+          hv[i] += v[b][i];
+        }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    tv[i] = (hv[i] + p.bm - 1) / p.bm;
     hsum += hv[i];
     tsum += tv[i];
   }

@@ -63,7 +63,7 @@ ALIGN_CASES = [
 ]
 
 
-@pytest.mark.parametrize("bm", [16, 64, 128])
+@pytest.mark.parametrize("bm", [16, 64, 128, 160, 256])
 @pytest.mark.parametrize("M,E,k,bias", ALIGN_CASES)
 def test_align_bit_exact(M, E, k, bias, bm):
     d = O.make_inputs(M, 8, 8, E, k, expert_bias_std=bias)
