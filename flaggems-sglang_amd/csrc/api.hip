@@ -6,6 +6,7 @@
 
 namespace fmoe {
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s);
+int decode_int4_row_split(int64_t max_tiles);
 int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
 int dequant_4bit(int wtype, const void* q, const void* scale, const void* zeros, int64_t E,
                  int64_t R, int64_t K, uint16_t* out, hipStream_t s);
@@ -141,7 +142,10 @@ extern "C" int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_rou
   }
   const int64_t slots = r->n_tokens * r->top_k;
   const int64_t est_tiles = slots < r->n_experts ? (slots > 0 ? slots : 1) : r->n_experts;
-  const int64_t ntiles = (K + kDecodeBN - 1) / kDecodeBN;
+  // row workgroups: 64 rows each, or (row blocks) x 64 for the int4 row-split kernel
+  const int rs = is_int4(wtype) ? decode_int4_row_split(r->max_tiles) : 0;
+  const int64_t bn = rs > 0 ? rs * kDecodeBN : kDecodeBN;
+  const int64_t ntiles = (K + bn - 1) / bn;
   const int64_t wgs = est_tiles * ntiles;
   const int64_t stage_elems = wtype == FMOE_W_BF16 ? 64 : 128;
   const int64_t nk = N / stage_elems;
@@ -358,6 +362,7 @@ FusedLayout layout(const fmoe_fused_args* a) {
   r.top_k = a->top_k;
   r.n_experts = a->E;
   r.block_m = L.bm;
+  r.max_tiles = static_cast<int32_t>(L.max_tiles);
   L.splits = fmoe_gemm2_splits(a->wtype, a->K, a->N, &r, 0);
   size_t off = 0;
   auto take = [&](size_t bytes) {

@@ -626,6 +626,228 @@ __global__ __launch_bounds__(kThreads * RB, (WT == WType::kInt4 && PIPE == 1 && 
   }
 }
 
+// int4 decode, row split: the workgroup's 4 waves each own one 64-row block
+// of the weights over the whole reduction range (of this split), all on the
+// same stage at a time, so the tile's 16-slot activation stage (4 KiB) is
+// loaded once per workgroup instead of once per wave: each wave brings a
+// quarter of it (4 rows) two stages ahead, through registers into a 3-slot
+// LDS ring published by one barrier per stage.  All global loads are ordinary
+// compiler-tracked loads.  Weights, scales / zeros and the arithmetic are the
+// row-block kernel's (one stage of weight registers reloaded piecewise).
+#ifndef FMOE_DECODE_RS_BLOCKS
+#define FMOE_DECODE_RS_BLOCKS 4
+#endif
+constexpr int kRsBlocks = FMOE_DECODE_RS_BLOCKS;  // row blocks (= waves) per workgroup
+constexpr int kRsThreads = 64 * kRsBlocks;
+constexpr int kRsPieces = 4 / kRsBlocks;          // activation loads per lane and stage
+static_assert(kRsBlocks == 1 || kRsBlocks == 2 || kRsBlocks == 4, "row blocks per workgroup");
+constexpr int kRsPitch = 256 + 16;  // LDS bytes per activation row (padded against bank conflicts)
+
+template <Mode MODE, int ACT>
+__global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_rs_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[3][BM * kRsPitch];
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
+  // workgroup -> (split, tile, group of 4 row blocks), XCD-contiguous as in
+  // gemm_decode_kernel (row blocks fastest when a tile has <= 128 of them)
+  const int gy = gridDim.y;
+  const int ntl = *p.n_tiles;
+  const int live = ntl * gy * gridDim.z;
+  const int b = blockIdx.x + gridDim.x * (blockIdx.y + gy * blockIdx.z);
+  if (b >= live) return;
+  const int L = xcd_remap(b, live);
+  const int split = L / (gy * ntl);
+  int mt, ntw;
+  if (gy * kRsBlocks <= 128) {
+    ntw = L % gy;
+    mt = (L / gy) % ntl;
+  } else {
+    mt = L % ntl;
+    ntw = (L / ntl) % gy;
+  }
+  const int nt = ntw * kRsBlocks + wid;  // this wave's 64-row block
+  const int tm = p.tile_map[mt];
+  const int e = tm & 0xffff;
+  const int row_beg = p.offs_raw[e] + (tm >> 16) * BM;
+  const int n_rows = min(p.offs_raw[e + 1], row_beg + BM) - row_beg;
+
+  // activation rows: piece h of this lane is row 16 wid / kRsBlocks + 4 h +
+  // lane / 16 (16 bytes of its 256-byte stage slice); fragments are read as
+  // the row-block kernel loads them (lane -> row lane % 16, bytes 64 (lane /
+  // 16) .. + 63)
+  const uint8_t* a_src[kRsPieces];
+  int a_dst[kRsPieces];
+#pragma unroll
+  for (int h = 0; h < kRsPieces; ++h) {
+    const int ar = (16 / kRsBlocks) * wid + 4 * h + (lane >> 4);
+    const int as = row_beg + (ar < n_rows ? ar : 0);
+    const int64_t a_row = MODE == Mode::kGemm1Silu ? p.topk_indx[as] / p.top_k : as;
+    a_src[h] = p.A + a_row * p.Kred * 2 + (lane & 15) * 16;
+    a_dst[h] = ar * kRsPitch + (lane & 15) * 16;
+  }
+  const int a_frag = (lane & 15) * kRsPitch + (lane >> 4) * 64;
+
+  const int64_t w_bytes = p.Kred / 2;
+  const int nk = static_cast<int>(p.Kred / 128);
+  const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * w_bytes;
+  int64_t wrow[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    int64_t r;
+    if (MODE == Mode::kGemm1Silu) {
+      int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + (lane & 15);
+      if (jj >= p.N_act) jj = p.N_act - 1;
+      r = gemm1_row(ACT, p.N_act, jj, j < NI / 2 ? 0 : 1);
+    } else {
+      r = static_cast<int64_t>(nt) * BN + j * 16 + (lane & 15);
+      if (r >= p.Nout) r = p.Nout - 1;
+    }
+    wrow[j] = r;
+  }
+  const bool tiled = p.b_tiled;
+  const int64_t w_stride = tiled ? 1024 : 64;  // bytes between a row's stages
+  const uint8_t* w_ptr[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+    w_ptr[j] = tiled ? Be + (wrow[j] >> 4) * 16 * w_bytes + (lane >> 4) * 256 + (wrow[j] & 15) * 16
+                     : Be + wrow[j] * w_bytes + (lane >> 4) * 16;
+  // group scales (lanes 0-31) / zeros (lanes 32-39) of the wave's rows, one
+  // dword per lane and stage (the row-block kernel's scheme)
+  const uint8_t* meta_ptr;
+  int64_t meta_stride;
+  {
+    const int ln = lane < 32 ? lane : (lane < 40 ? lane - 32 : 0);
+    const int j = lane < 32 ? ln / 8 : ln / 2;
+    const int r = lane < 32 ? (2 * ln) % 16 : 8 * (ln % 2);
+    int64_t row;
+    if (MODE == Mode::kGemm1Silu) {
+      int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + r;
+      if (jj >= p.N_act) jj = p.N_act - 8;
+      row = gemm1_row(ACT, p.N_act, jj, j < NI / 2 ? 0 : 1);
+    } else {
+      row = static_cast<int64_t>(nt) * BN + j * 16 + r;
+      if (row >= p.Nout) row = p.Nout - 8;
+    }
+    const int64_t ebase = static_cast<int64_t>(e) * (p.Kred / 128) * p.Nout + row;
+    if (lane < 32) {
+      meta_ptr = reinterpret_cast<const uint8_t*>(p.b_gscale) + 2 * ebase;
+      meta_stride = 2 * p.Nout;
+    } else {
+      meta_ptr = p.b_zero + (ebase >> 1);
+      meta_stride = p.Nout / 2;
+    }
+  }
+
+  f32x4_t acc[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int per_split = (nk + p.splits - 1) / p.splits;
+  const int k_beg = min(nk, split * per_split);
+  const int n = min(nk, k_beg + per_split) - k_beg;  // stages of this split (same for every wave)
+  i32x4_t an[kRsPieces];  // this lane's pieces of a later activation stage
+  i32x4_t wb[NI];
+  int meta = 0;
+  int64_t woff = static_cast<int64_t>(k_beg) * w_stride;
+  const uint8_t* mp = meta_ptr + k_beg * meta_stride;
+  if (n > 0) {
+#pragma unroll
+    for (int h = 0; h < kRsPieces; ++h) {
+      an[h] = *reinterpret_cast<const i32x4_t*>(a_src[h] + static_cast<int64_t>(k_beg) * 256);
+      *reinterpret_cast<i32x4_t*>(&a_lds[0][a_dst[h]]) = an[h];
+      if (n > 1) an[h] = *reinterpret_cast<const i32x4_t*>(a_src[h] + static_cast<int64_t>(k_beg + 1) * 256);
+    }
+#pragma unroll
+    for (int j = 0; j < NI; ++j) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+    if (lane < 40) meta = *reinterpret_cast<const int*>(mp);
+  }
+  __syncthreads();
+  const int r16 = lane & 15;
+  const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
+  for (int i = 0; i < n; ++i) {
+    const int kt = k_beg + i;
+    const bool more = i + 1 < n;
+    // publish stage kt + 1 (its slot was last read at stage kt - 2), fetch
+    // this lane's piece of stage kt + 2
+#pragma unroll
+    for (int h = 0; h < kRsPieces; ++h) {
+      if (more) *reinterpret_cast<i32x4_t*>(&a_lds[(i + 1) % 3][a_dst[h]]) = an[h];
+      if (i + 2 < n) an[h] = *reinterpret_cast<const i32x4_t*>(a_src[h] + static_cast<int64_t>(kt + 2) * 256);
+    }
+    woff += w_stride;
+    mp += meta_stride;
+    unsigned sw[NI], zw[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      sw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), meta));
+      zw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), meta));
+    }
+    if (more && lane < 40) meta = *reinterpret_cast<const int*>(mp);
+    // activations of stage kt, permuted to the (j, j+4) nibble pairing
+    const uint8_t* af = &a_lds[i % 3][a_frag];
+    bf16x8_t a[4];
+    f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(af + 16 * d);
+      a[d] = as_bf16x8(__builtin_amdgcn_perm(v[2], v[0], 0x05040100), __builtin_amdgcn_perm(v[2], v[0], 0x07060302),
+                       __builtin_amdgcn_perm(v[3], v[1], 0x05040100), __builtin_amdgcn_perm(v[3], v[1], 0x07060302));
+      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], ones, xs, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const unsigned wv = static_cast<unsigned>(wb[j][d]);
+        const int b0 = static_cast<int>((wv & 0x000f000fu) | 0x43004300u);
+        const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
+        const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
+        const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
+      }
+      if (more) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+      const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw[j] >> 16) : (sw[j] & 0xffffu))));
+      const float z = static_cast<float>((zw[j] >> (4 * (r16 & 7))) & 15u);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[r] - (128.0f + z) * xs[r]);
+    }
+    __syncthreads();  // stage kt + 1 visible; stage kt's slot free from stage kt + 2 on
+  }
+
+  // ---- epilogue: this wave's rows (the row-block kernel's, without the
+  // cross-wave reduction)
+  const int col16 = lane & 15;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int rr = (lane >> 4) * 4 + r;
+    if (rr >= n_rows) continue;
+    const int s = row_beg + rr;
+    const float g = p.gamma ? p.gate_scal[s] : 1.0f;
+    if (MODE == Mode::kGemm1Silu) {
+      uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.N_act;
+#pragma unroll
+      for (int j = 0; j < NI / 2; ++j) {
+        const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + j * 16 + col16;
+        if (col >= p.N_act) continue;
+        float gb, ub;
+        gemm1_bias<ACT>(p, e, col, gb, ub);
+        act[col] = f32_to_bf16(gemm1_act<ACT>(p, acc[j][r], acc[j + NI / 2][r], gb, ub, g));
+      }
+    } else {
+      float* y = static_cast<float*>(p.out) + split * p.out_split_stride + static_cast<int64_t>(s) * p.Nout;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int64_t col = static_cast<int64_t>(nt) * BN + j * 16 + col16;
+        if (col < p.Nout) {
+          const float bb = (p.bias && split == 0) ? p.bias[static_cast<int64_t>(e) * p.Nout + col] : 0.f;
+          y[col] = (acc[j][r] + bb) * g;
+        }
+      }
+    }
+  }
+}
+
 }  // namespace decode
 
 // Row blocks per workgroup by format and GEMM (build-time overridable for
@@ -654,6 +876,20 @@ static_assert(decode_row_blocks(WType::kBf16) >= 1 && decode_row_blocks(WType::k
                   decode_row_blocks(WType::kMxfp4) >= 1 && decode_row_blocks(WType::kMxfp4) <= decode::kMaxRB,
               "decode row blocks out of range");
 
+// int4 with the align launch and many tiles: the row-split kernel (one
+// activation stage per workgroup) instead of the row-block kernel.  Measured
+// on Mixtral W4A16 (tiled): M=64 (15 tiles) 254 -> 244 us; at M=4 / 16 (<= 9
+// tiles) its 4x coarser workgroups balance worse: 13% / 5% slower there.
+#ifndef FMOE_DECODE_INT4_RS
+#define FMOE_DECODE_INT4_RS 1
+#endif
+constexpr int kRsMinTiles = 14;
+// row blocks per workgroup of the int4 row-split kernel for a grid of
+// max_tiles expert tiles, 0 when the row-block kernel runs
+int decode_int4_row_split(int64_t max_tiles) {
+  return FMOE_DECODE_INT4_RS != 0 && max_tiles >= kRsMinTiles ? decode::kRsBlocks : 0;
+}
+
 int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   GemmParams p = p0;
   const int64_t ncols = mode == Mode::kGemm1Silu ? p.N_act : p.Nout;
@@ -664,6 +900,19 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   if (p.max_tiles <= 0) return FMOE_OK;
   dim3 g(static_cast<unsigned>(p.max_tiles), static_cast<unsigned>(p.n_ntiles),
          static_cast<unsigned>(mode == Mode::kGemm2 ? p.splits : 1));
+  if (wt == WType::kInt4 && !p.tiny_ids && decode_int4_row_split(p.max_tiles) > 0) {
+    g.y = static_cast<unsigned>((nblocks + decode::kRsBlocks - 1) / decode::kRsBlocks);
+    const dim3 b(decode::kRsThreads);
+    if (mode == Mode::kGemm2)
+      decode::gemm_decode_int4_rs_kernel<Mode::kGemm2, kActSilu><<<g, b, 0, s>>>(p);
+    else if (p.act == kActSwiglu)
+      decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSwiglu><<<g, b, 0, s>>>(p);
+    else if (p.act == kActGelu)
+      decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActGelu><<<g, b, 0, s>>>(p);
+    else
+      decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSilu><<<g, b, 0, s>>>(p);
+    return fmoe_host::check_launch("gemm_decode_int4_rs");
+  }
 #define LAUNCH(WT_, MODE_, ACT_)                                                                      \
   do {                                                                                                \
     constexpr int RB_ = decode_row_blocks(WT_);                                                       \
