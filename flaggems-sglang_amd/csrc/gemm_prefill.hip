@@ -308,6 +308,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   const float* sa_src = nullptr;
   if (sa_wave) sa_src = p.a_scale + a_src_row(min(64 * sa_j + lane, BM - 1)) * ksb + k0;
   // fp8 weight scales of the whole k range, staged once in LDS
+  int sb_split = NI;  // GEMM2: 16-row blocks of the wave under its first weight-scale block
   if (FP8) {
     const int64_t nrb = p.Nout / 128;
     const float* se = p.b_scale + static_cast<int64_t>(e) * nrb * ksb;
@@ -319,10 +320,14 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       s0 = se + (gemm1_row(ACT, p.N_act, j, 0) / 128) * ksb;
       s1 = se + (gemm1_row(ACT, p.N_act, j, 1) / 128) * ksb;
     } else {
+      // the wave's rows span at most two 128-row scale blocks (WN <= 128):
+      // 16-row blocks j < sb_split use the first one
       int64_t j = static_cast<int64_t>(nt) * BN + wn * WN;
       if (j >= p.Nout) j = p.Nout - 1;
+      const int64_t jl = min(j + WN - 1, p.Nout - 1);
       s0 = se + (j / 128) * ksb;
-      s1 = s0;
+      s1 = se + (jl / 128) * ksb;
+      if (jl / 128 != j / 128) sb_split = static_cast<int>((128 - j % 128) / 16);
     }
     if (wm == 0)
       for (int kk = lane; kk < nk; kk += kWave) {
@@ -383,7 +388,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
         for (int j = 0; j < NI; ++j) {
           f32x4_t t = {0.f, 0.f, 0.f, 0.f};
           t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fa[i], fb[j], t, 0, 0, 0, 0, 0, 0);
-          const float sb = (MODE == Mode::kGemm1Silu && j >= NI / 2) ? sb1 : sb0;
+          const float sb = (MODE == Mode::kGemm1Silu ? j >= NI / 2 : j >= sb_split) ? sb1 : sb0;
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[i][j][r] += t[r] * (sa[r] * sb);
         }
@@ -601,7 +606,8 @@ int launch(const GemmParams& p0, hipStream_t s) {
 //   bf16: BM 256 -> 256x256, 4x2 waves, 128-byte stages, 2-deep ring
 //         BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM  64 ->  64x256, 1x4 waves, 64-byte stages, 4-deep ring
-//   fp8 : BM 160 -> 160x256, 2x4 waves, 128-byte stages, 3-deep ring (K <= 8192)
+//   fp8 : BM 160 -> GEMM1 160x256, 3-deep ring; GEMM2 160x384, 2-deep ring;
+//                   2x4 waves, 128-byte stages (K, N <= 8192)
 //         BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM  64 ->  64x256, 1x8 waves, 128-byte stages, 3-deep ring
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s) {
@@ -615,6 +621,10 @@ int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t
     if (bm == 128) return L(128, 256, 2, 4, 128, 3, false);
     if (bm == 64) return L(64, 256, 1, 4, 64, 4, false);
   } else {
+    // GEMM2 with 160-row tiles: 384-wide output tiles (2-deep ring of 68 KiB
+    // stages), so the activation tile is re-read by a third fewer N-tiles
+    // (13% fewer operand requests per output; DSV3 GEMM2 M=4096 -5%, M=8192 -7%)
+    if (bm == 160 && mode == Mode::kGemm2) return launch<Cfg<160, 384, 2, 4, 128, 2, true, Mode::kGemm2>>(p, s);
     if (bm == 160) return L(160, 256, 2, 4, 128, 3, true);
     if (bm == 128) return L(128, 256, 2, 4, 128, 3, true);
     if (bm == 64) return L(64, 256, 1, 8, 128, 3, true);
