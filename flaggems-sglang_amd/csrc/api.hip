@@ -91,7 +91,7 @@ GemmParams base_params(const fmoe_routing* r) {
 // Tile height for the fused path: 16 = decode kernels, else the prefill tile,
 // from the mean slots per expert (measured on the BASELINE shapes): bf16
 // 256-row tiles once experts average >= 256 slots, 128-row tiles from 40
-// (a half-empty 128-row tile still beats a 64-row one), else 64; fp8 160-row
+// (a half-empty 128-row tile still beats a 64-row one), else 64; 160-row
 // tiles as below.
 int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
   const int64_t slots = M * k;
@@ -101,10 +101,10 @@ int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
   const int64_t mean = slots / E;
   if (wtype == FMOE_W_BF16 && mean >= 256) return 256;
   if (mean < 40) return 64;
-  if (wtype == FMOE_W_FP8) {
-    // fp8: 160-row tiles where they need fewer M-tiles per expert than
-    // 128-row ones at the mean + 2 sd of a uniform routing's per-expert load
-    // (each M-tile streams the expert's whole weight panel again)
+  if (wtype == FMOE_W_FP8 || wtype == FMOE_W_BF16) {
+    // 160-row tiles where they need fewer M-tiles per expert than 128-row
+    // ones at the mean + 2 sd of a uniform routing's per-expert load (each
+    // M-tile streams the expert's whole weight panel again)
     const double q = static_cast<double>(mean) + 2.0 * std::sqrt(static_cast<double>(mean));
     if (std::ceil(q / 160.0) < std::ceil(q / 128.0)) return 160;
   }
@@ -112,8 +112,10 @@ int choose_block_m(int wtype, int64_t M, int k, int E, int path) {
 }
 
 // The 160-row fp8 tile stages the weight scales of at most 64 reduction
-// blocks (K, N <= 8192); larger layers take 128-row tiles.
-int fit_block_m(int bm, int64_t K, int64_t N) { return bm == 160 && (K > 8192 || N > 8192) ? 128 : bm; }
+// blocks (K, N <= 8192); larger fp8 layers take 128-row tiles.
+int fit_block_m(int wtype, int bm, int64_t K, int64_t N) {
+  return wtype == FMOE_W_FP8 && bm == 160 && (K > 8192 || N > 8192) ? 128 : bm;
+}
 
 }  // namespace
 
@@ -355,7 +357,7 @@ int check_fused(const fmoe_fused_args* a) {
 FusedLayout layout(const fmoe_fused_args* a) {
   FusedLayout L{};
   const int64_t slots = a->M * a->top_k;
-  L.bm = fit_block_m(choose_block_m(a->wtype, a->M, a->top_k, a->E, a->path), a->K, a->N);
+  L.bm = fit_block_m(a->wtype, choose_block_m(a->wtype, a->M, a->top_k, a->E, a->path), a->K, a->N);
   L.max_tiles = fmoe_max_tiles(slots, a->E);
   fmoe_routing r{};
   r.n_tokens = a->M;

@@ -604,6 +604,7 @@ int launch(const GemmParams& p0, hipStream_t s) {
 
 // Host launcher: picks the instantiation for the tile height.
 //   bf16: BM 256 -> 256x256, 4x2 waves, 128-byte stages, 2-deep ring
+//         BM 160 -> 160x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM 128 -> 128x256, 2x4 waves, 128-byte stages, 3-deep ring
 //         BM  64 ->  64x256, 1x4 waves, 64-byte stages, 4-deep ring
 //   fp8 : BM 160 -> GEMM1 160x256, 3-deep ring; GEMM2 160x384, 2-deep ring;
@@ -618,6 +619,7 @@ int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t
                             : launch<Cfg<BM, BN, WMS, WNS, SB, NB, F8, Mode::kGemm2>>(p, s))
   if (!fp8) {
     if (bm == 256) return L(256, 256, 4, 2, 128, 2, false);
+    if (bm == 160) return L(160, 256, 2, 4, 128, 3, false);
     if (bm == 128) return L(128, 256, 2, 4, 128, 3, false);
     if (bm == 64) return L(64, 256, 1, 4, 64, 4, false);
   } else {

@@ -247,8 +247,8 @@ int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale, const void
 
 /* Tile height the library pairs with the GEMM kernels for a problem size:
  * 16 selects the decode (streaming) kernels, 64 / 128 / 160 / 256 the prefill
- * kernels (160: fp8 only, for K and N <= 8192 -- the caller substitutes 128
- * above that; fmoe_fused_experts does so itself).
+ * kernels (256: bf16 only; 160 with fp8 weights needs K and N <= 8192 -- the
+ * caller substitutes 128 above that; fmoe_fused_experts does so itself).
  * path: 0 = choose, 1 = prefill, 2 = decode (4-bit weights always report 16:
  * their large-batch route dequantizes to bf16 inside fmoe_fused_experts). */
 int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path);
