@@ -180,6 +180,27 @@ def test_fp8_tile_height_choice(K, N):
     _close(out2, ref, 5e-2)
 
 
+def test_bf16_160_row_tiles_skewed():
+    """bf16 prefill at 128 slots per expert on average takes 160-row tiles;
+    skewed routing gives experts that need two of them and nearly empty
+    ones, and K = 384 is not a multiple of the 256-wide output tile.  Fused
+    and stage paths against the oracle."""
+    M, K, N, E, k = 512, 384, 640, 8, 2
+    from flaggems_sglang import _lib as LB
+    assert LB.lib().fmoe_choose_block_m(LB.W_BF16, M, k, E, 0) == 160
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05, expert_bias_std=0.7)
+    counts = torch.bincount(d["topk_ids"].flatten().long(), minlength=E)
+    assert int(counts.max()) > 160 and int(counts.min()) < 128
+    tw, ti = d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    ref = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"])
+    out = flaggems_sglang.fused_experts(d["x"].to(DEV), d["w13"].to(DEV), d["w2"].to(DEV), tw, ti)
+    _close(out, ref, 2e-2)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw, ti, E)
+    out2 = flaggems_sglang.triton_kernel_fused_experts(
+        d["x"].to(DEV), d["w13"].transpose(1, 2).to(DEV), d["w2"].transpose(1, 2).to(DEV), rd, gi, si)
+    _close(out2, ref, 2e-2)
+
+
 @pytest.mark.parametrize("M", [1, 4, 16, 64])
 def test_mixtral_w4a16(M):
     K, N, E, k = 4096, 14336, 8, 2
