@@ -48,10 +48,12 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
 // out[t, c] = bf16(scale * sum_j sum_p y[p][gate_indx[t*k+j], c]): the
 // token's k slots in ascending j, each slot's split planes in ascending p,
 // one running fp32 sum per column in exactly that order (deterministic).
-// One thread = 4 columns (16-byte loads); the (j, p) terms are fetched
-// kBatch at a time so their loads are in flight together.
+// One thread = 4 columns (16-byte loads).  The (j, p) terms are taken BATCH
+// at a time: first every term's slot (the gate_indx loads together), then
+// every term's row load -- dropped slots read a row that exists and is not
+// added -- so the loads of a batch are in flight together; then the adds in
+// order.  Small calls (k * splits <= 32, decode) take all terms in one batch.
 constexpr int kSumThreads = 256;
-constexpr int kBatch = 8;
 
 template <typename YT>
 __device__ __forceinline__ void load4(const YT* src, float (&v)[4]) {
@@ -70,7 +72,7 @@ __device__ __forceinline__ void load4(const YT* src, float (&v)[4]) {
   }
 }
 
-template <typename YT>
+template <typename YT, int BATCH>
 __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restrict__ y, int splits,
                                                               int64_t split_stride,
                                                               const int32_t* __restrict__ gate_indx,
@@ -83,31 +85,38 @@ __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restri
   // tokens t = blockIdx.y, blockIdx.y + gridDim.y, ... (grid y is capped at 65535)
   for (int64_t t = blockIdx.y; t < n_tok; t += gridDim.y) {
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    int j = 0, p = 0;  // (slot, plane) of the batch's first term
-    for (int b = 0; b < n_terms; b += kBatch) {
-      float v[kBatch][4];
-      bool live[kBatch];
+    for (int b = 0; b < n_terms; b += BATCH) {
+      // slot of each term: tiny-batch path (gate_indx null) = flat index t k
+      // + j, dropped when its expert id is out of range; else gate_indx (< 0:
+      // dropped)
+      int row[BATCH];
+      bool live[BATCH];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
+      for (int u = 0; u < BATCH; ++u) {
+        const int q = b + u;
         live[u] = false;
-        if (b + u < n_terms) {
-          // tiny-batch path (gate_indx null): slot = flat index, dropped when
-          // its expert id is out of range; else a negative slot is dropped
-          const int64_t f = t * k + j;
-          const int sl = gate_indx ? gate_indx[f]
-                                   : (ids[f] >= 0 && ids[f] < n_experts ? static_cast<int>(f) : -1);
-          if (sl >= 0) {
-            load4(y + p * split_stride + static_cast<int64_t>(sl) * K + c, v[u]);
-            live[u] = true;
+        row[u] = static_cast<int>(t * k);
+        if (q < n_terms) {
+          const int64_t f = t * k + q / splits;
+          int sl;
+          if (gate_indx) {
+            sl = gate_indx[f];
+          } else {
+            const int id = ids[f];
+            sl = id >= 0 && id < n_experts ? static_cast<int>(f) : -1;
           }
-          if (++p == splits) {
-            p = 0;
-            ++j;
-          }
+          live[u] = sl >= 0;
+          if (sl >= 0) row[u] = sl;  // else a row that exists, not added
         }
       }
+      float v[BATCH][4];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u)
+      for (int u = 0; u < BATCH; ++u) {
+        const int q = b + u;  // uniform: terms past the last one issue no load
+        if (q < n_terms) load4(y + (q % splits) * split_stride + static_cast<int64_t>(row[u]) * K + c, v[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; ++u)
         if (live[u]) {
           acc[0] += v[u][0];
           acc[1] += v[u][1];
@@ -163,8 +172,12 @@ extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
-  moe_sum_kernel<float><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
-      y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
+  if (k * splits <= 32)
+    moe_sum_kernel<float, 32><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
+        y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
+  else
+    moe_sum_kernel<float, 8><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
+        y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 
@@ -174,8 +187,12 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
                  float scale, void* out, hipStream_t s) {
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
-  moe_sum_kernel<float><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
-                                        static_cast<uint16_t*>(out));
+  if (k * splits <= 32)
+    moe_sum_kernel<float, 32><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
+                                              static_cast<uint16_t*>(out));
+  else
+    moe_sum_kernel<float, 8><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
+                                             static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 // moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
@@ -183,7 +200,7 @@ int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, 
                  float scale, void* out, hipStream_t s) {
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
-  moe_sum_kernel<__bf16><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
+  moe_sum_kernel<__bf16, 8><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
                                          nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
