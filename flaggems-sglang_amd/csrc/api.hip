@@ -14,6 +14,9 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
                  float scale, void* out, hipStream_t s);
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s);
+int launch_fused_int4(const GemmParams& p, const GemmParams& q, hipStream_t s);
+int moe_sum_planes(const float* y, int planes, const int32_t* gate_indx, const int32_t* ids, int E,
+                   int64_t M, int k, int64_t K, float scale, void* out, hipStream_t s);
 }  // namespace fmoe
 
 using namespace fmoe;
@@ -210,6 +213,10 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
   if (int st = check_epilogue(ep, "gemm1")) return st;
   if (int st = check_routing(r, "gemm1")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm1: unknown weight type %d", wtype);
+  // (the int4 kernels' per-stage scale / zero fetch assumes adjacent gate
+  // and up rows are the split halves, not SWIGLU's interleaved pairs)
+  if (is_int4(wtype) && ep && ep->activation == FMOE_ACT_SWIGLU)
+    return fail(FMOE_ERR_UNSUPPORTED, "gemm1: int4 weights with SWIGLU are not supported");
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
     return fail(FMOE_ERR_UNSUPPORTED, "gemm1: K=%lld N=%lld must be multiples of 128",
                 static_cast<long long>(K), static_cast<long long>(N));
@@ -332,6 +339,7 @@ struct FusedLayout {
   int bm;
   int splits;
   bool y_bf16;
+  bool fused4;  // one-launch int4 decode (splits = N / 128 planes)
   int64_t max_tiles;
   size_t align_ws, expt_indx, expt_scal, topk_indx, gate_indx, gate_scal, hist, offs_raw,
       offs_pad, tile_map, n_tiles, xq, xs, act, actq, acts, y, lut, total;
@@ -345,6 +353,8 @@ int check_fused(const fmoe_fused_args* a) {
   if (a->K <= 0 || a->N <= 0 || a->K % 128 != 0 || a->N % 128 != 0)
     return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: K=%lld N=%lld must be multiples of 128",
                 static_cast<long long>(a->K), static_cast<long long>(a->N));
+  if (is_int4(a->wtype) && a->activation == FMOE_ACT_SWIGLU)
+    return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: int4 weights with SWIGLU are not supported");
   if (is_int4(a->wtype) && a->group_size != 128)
     return fail(FMOE_ERR_UNSUPPORTED, "fused_experts: int4 group_size=%d is not supported",
                 a->group_size);
@@ -352,6 +362,19 @@ int check_fused(const fmoe_fused_args* a) {
   fmoe_epilogue ep{a->activation, a->b13, a->alpha, a->limit};
   if (int st = check_epilogue(&ep, "fused_experts")) return st;
   return FMOE_OK;
+}
+
+// Tiled int4 decode of the smallest batches runs as one launch per call
+// (fused_int4_kernel: GEMM1, activation and GEMM2 of a 128-column slice of
+// the intermediate per workgroup) plus the plane sum.  Its N / 128 fp32
+// partial planes per slot grow with M, so larger batches keep the two GEMM
+// launches.
+#ifndef FMOE_FUSED_INT4_MAX_M
+#define FMOE_FUSED_INT4_MAX_M 1
+#endif
+bool fused_int4_route(const fmoe_fused_args* a, int bm) {
+  return a->wtype == FMOE_W_INT4_TILED && bm == kDecodeBM && a->activation != FMOE_ACT_SWIGLU &&
+         a->M <= FMOE_FUSED_INT4_MAX_M && a->top_k <= 32;
 }
 
 FusedLayout layout(const fmoe_fused_args* a) {
@@ -365,7 +388,8 @@ FusedLayout layout(const fmoe_fused_args* a) {
   r.n_experts = a->E;
   r.block_m = L.bm;
   r.max_tiles = static_cast<int32_t>(L.max_tiles);
-  L.splits = fmoe_gemm2_splits(a->wtype, a->K, a->N, &r, 0);
+  L.fused4 = fused_int4_route(a, L.bm);
+  L.splits = L.fused4 ? static_cast<int>(a->N / 128) : fmoe_gemm2_splits(a->wtype, a->K, a->N, &r, 0);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t o = off;
@@ -416,20 +440,14 @@ bool tiny_decode(const fmoe_fused_args* a, const FusedLayout& L) {
          !a->expert_map;
 }
 
-int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStream_t s) {
-  const int64_t slots = a->M * a->top_k;
-  GemmParams g1{};
-  g1.top_k = a->top_k;
-  g1.n_experts = a->E;
-  g1.max_tiles = static_cast<int>(fmoe_max_tiles(slots, a->E));
+// GEMM1 / GEMM2 parameters of the fused decode path; g1 comes in with the
+// routing fields set (tile map or tiny-batch ids), g2 starts as its copy.
+void decode_pair(const fmoe_fused_args* a, const FusedLayout& L, char* ws, GemmParams& g1, GemmParams& g2) {
   g1.splits = 1;
   g1.alpha = a->alpha;
   g1.limit = a->limit;
   g1.act = a->activation;
-  g1.tiny_ids = a->topk_ids;
-  g1.tiny_w = a->topk_weights;
-  g1.n_tokens = a->M;
-  GemmParams g2 = g1;
+  g2 = g1;
   g1.A = static_cast<const uint8_t*>(a->x);
   g1.B = static_cast<const uint8_t*>(a->w13);
   g1.b_scale = static_cast<const float*>(a->w13_scale);
@@ -443,7 +461,6 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g1.gamma = a->apply_router_weight_on_input;
   g1.bias = a->b13;
   g1.out = ws + L.act;
-  if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm1Silu, g1, s)) return st;
   g2.act = FMOE_ACT_SILU;
   g2.A = static_cast<const uint8_t*>(g1.out);
   g2.B = static_cast<const uint8_t*>(a->w2);
@@ -459,10 +476,29 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
   g2.bias = a->b2;
   g2.out = ws + L.y;
   g2.splits = L.splits;
-  g2.out_split_stride = slots * a->K;
+  g2.out_split_stride = a->M * a->top_k * a->K;
+}
+
+int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStream_t s) {
+  const int64_t slots = a->M * a->top_k;
+  GemmParams g1{}, g2;
+  g1.top_k = a->top_k;
+  g1.n_experts = a->E;
+  g1.max_tiles = static_cast<int>(fmoe_max_tiles(slots, a->E));
+  g1.tiny_ids = a->topk_ids;
+  g1.tiny_w = a->topk_weights;
+  g1.n_tokens = a->M;
+  decode_pair(a, L, ws, g1, g2);
+  const float* y = reinterpret_cast<const float*>(ws + L.y);
+  if (L.fused4) {
+    if (int st = launch_fused_int4(g1, g2, s)) return st;
+    return moe_sum_planes(y, L.splits, nullptr, a->topk_ids, a->E, a->M, a->top_k, a->K,
+                          a->routed_scaling_factor, a->out, s);
+  }
+  if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm1Silu, g1, s)) return st;
   if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm2, g2, s)) return st;
-  return moe_sum_flat(reinterpret_cast<const float*>(ws + L.y), L.splits, a->topk_ids, a->E, a->M,
-                      a->top_k, a->K, a->routed_scaling_factor, a->out, s);
+  return moe_sum_flat(y, L.splits, a->topk_ids, a->E, a->M, a->top_k, a->K, a->routed_scaling_factor,
+                      a->out, s);
 }
 
 }  // namespace
@@ -589,6 +625,14 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
       return st;
     x = at(L.xq);
     xs = static_cast<const float*>(at(L.xs));
+  }
+  if (L.fused4) {
+    GemmParams g1 = base_params(&r), g2;
+    decode_pair(a, L, ws, g1, g2);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int st = launch_fused_int4(g1, g2, s)) return st;
+    return moe_sum_planes(static_cast<const float*>(at(L.y)), L.splits, o.gate_indx, nullptr, a->E, a->M,
+                          a->top_k, a->K, a->routed_scaling_factor, a->out, s);
   }
   fmoe_epilogue ep{a->activation, a->b13, a->alpha, a->limit};
   int4* lut = L.bm == kDecodeBM ? nullptr : static_cast<int4*>(at(L.lut));

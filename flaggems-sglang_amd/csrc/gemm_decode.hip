@@ -122,13 +122,14 @@ struct TinyLds {
   int ids[kTinySlots];
   int rows[BM];
   int info[4];     // expert, block, rows in the tile, valid
-  int scan[kWaves * kMaxRB];
+  int scan[16];    // one entry per wave (up to 16 waves)
 };
 
 // Returns false when tile mt does not exist (same decision in every thread).
 // NT = threads of the workgroup.
 template <int NT>
 __device__ bool tiny_route(const GemmParams& p, int mt, TinyLds& L) {
+  static_assert(NT % kWave == 0 && NT / kWave <= 16, "tiny_route: up to 16 waves");
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
   const int E = p.n_experts;
   const int n = static_cast<int>(p.n_tokens * p.top_k);
@@ -848,6 +849,301 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
   }
 }
 
+// ---------------------------------------------------------------------------
+// int4 (tiled) decode in one launch per call: GEMM1, the activation and GEMM2
+// of one 128-column slice of the intermediate dim in one workgroup.
+//
+// Workgroup (chunk c, tile mt) computes act[:, 128 c .. 128 c + 127] of the
+// tile's slots -- GEMM1 over the whole hidden dim for 256 weight rows: 4 row
+// blocks of 64 (the row-block kernel's, SiLU / GELU layout), each split over
+// 4 waves by interleaved stages, i.e. the 16 waves of four row-block
+// workgroups -- rounds it to bf16 into LDS (the rounding point of the
+// two-launch path), then multiplies it by w2[:, 128 c .. 128 c + 127]: one
+// 128-element quantization group of every w2 row, one 1 KiB tiled block per
+// 16 rows.  The product goes to partial plane c, y[c][slot][0 .. K), which
+// moe_sum_planes adds in fixed order.  No workgroup waits for another.
+// Against GEMM1 -> act -> GEMM2 as two launches this saves a launch, the
+// act round trip and the second kernel's ramp, for N / 128 partial planes of
+// fp32 rows (3.7 MB for one Mixtral token): a small-batch route.
+// dword 3 of a raw (untyped, stride 0) buffer descriptor on gfx950: offsets
+// at or past num_records are dropped by the hardware
+constexpr int kBufferDword3 = 0x00020000;
+constexpr int kFzWaves = 16;
+constexpr int kFzThreads = kFzWaves * kWave;
+constexpr int kFzCols = 128;                      // act columns per workgroup
+constexpr int kFzRowBlocks = kFzCols / (BN / 2);  // GEMM1 64-row blocks per workgroup
+constexpr int kFzKw = kFzWaves / kFzRowBlocks;    // waves per row block
+constexpr int kFzPitch = 2 * kFzCols + 16;        // LDS bytes per act row (padded)
+#ifndef FMOE_FUSED_INT4_BATCH
+#define FMOE_FUSED_INT4_BATCH 4
+#endif
+constexpr int kFzBatch = FMOE_FUSED_INT4_BATCH;   // w2 16-row groups per load batch
+constexpr int kFzBatchRows = 16 * kFzBatch;
+static_assert(kFzBatch == 4 || kFzBatch == 8, "w2 batch: 64 or 128 rows");
+static_assert(kFzKw == kWaves && kFzRowBlocks == 4, "fused int4 geometry");
+
+// One batch of 16 kFzBatch w2 rows at the workgroup's group c: kFzBatch tiled
+// blocks (16 bytes per lane each), their fp16 scales (one dword = 2 rows per
+// lane) and uint4 zeros (one dword = 8 rows per lane).
+struct W2Batch {
+  i32x4_t w[kFzBatch];
+  int sm, zm;
+};
+
+template <int ACT, bool TINY>
+__global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p, GemmParams q) {
+  static_assert(ACT != kActSwiglu, "int4 decode: SiLU / GELU row layout only");
+  __shared__ f32x4_t red[kFzKw - 1][kFzRowBlocks][NI][kWave];
+  __shared__ __attribute__((aligned(16))) uint8_t act_lds[BM * kFzPitch];
+  __shared__ TinyLds tiny_lds[1];
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int rb = wid % kFzRowBlocks, kw = wid / kFzRowBlocks;
+  const int c = blockIdx.x, mt = blockIdx.y;
+
+  int e, row_beg = 0, n_rows;
+  if constexpr (TINY) {
+    if (!tiny_route<kFzThreads>(p, mt, tiny_lds[0])) return;
+    e = tiny_lds[0].info[0];
+    n_rows = tiny_lds[0].info[2];
+  } else {
+    if (mt >= *p.n_tiles) return;
+    const int tm = p.tile_map[mt];
+    e = tm & 0xffff;
+    row_beg = p.offs_raw[e] + (tm >> 16) * BM;
+    n_rows = min(p.offs_raw[e + 1], row_beg + BM) - row_beg;
+  }
+  auto slot_of = [&](int r) { return TINY ? tiny_lds[0].rows[r] : row_beg + r; };
+  const int r16 = lane & 15;
+  // GEMM2 output slots of this lane (tile rows 4 (lane / 16) + r) and their
+  // gammas, loaded here so that they have long arrived when the GEMM2 loop
+  // (whose waits must not cover them) stores
+  int ys[4];
+  float yg[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = (lane >> 4) * 4 + r;
+    ys[r] = m < n_rows ? slot_of(m) : -1;
+    yg[r] = (ys[r] >= 0 && q.gamma) ? (TINY ? q.tiny_w[ys[r]] : q.gate_scal[ys[r]]) : 1.0f;
+  }
+
+  // ---- GEMM1 addresses (the row-block kernel's, 64-row block nt)
+  const int nt = c * kFzRowBlocks + rb;
+  const int s_a = slot_of(r16 < n_rows ? r16 : 0);
+  const int64_t a_row = (TINY ? s_a : p.topk_indx[s_a]) / p.top_k;
+  const uint8_t* ap = p.A + a_row * p.Kred * 2 + (lane >> 4) * 64;
+  const int64_t w_bytes = p.Kred / 2;
+  const int nk = static_cast<int>(p.Kred / 128);
+  const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * w_bytes;
+  // weight rows of block j: gate rows 32 nt + 16 j + r16 (j < 2), up rows N
+  // further; one per-lane base plus a uniform offset per block
+  const uint8_t* w_ptr0 = Be + (static_cast<int64_t>(nt) * (BN / 2) / 16) * 16 * w_bytes + (lane >> 4) * 256 + r16 * 16;
+  int64_t w_joff[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) w_joff[j] = ((j % (NI / 2)) * 16 + (j < NI / 2 ? 0 : p.N_act)) * w_bytes;
+  // scales (lanes 0-31: rows 2 d, 2 d + 1 of the virtual 16 j + r order) and
+  // zeros (lanes 32-39: rows 8 z .. 8 z + 7), one dword per lane and stage:
+  // element index mrow + kt N_out of the expert's [K / 128][N_out] arrays
+  // (uniform bases, a 32-bit per-lane index: no 64-bit pointer per lane)
+  int mrow;
+  {
+    const int ln = lane < 32 ? lane : (lane < 40 ? lane - 32 : 0);
+    const int j = lane < 32 ? ln / 8 : ln / 2;
+    const int r = lane < 32 ? (2 * ln) % 16 : 8 * (ln % 2);
+    const int64_t jj = static_cast<int64_t>(nt) * (BN / 2) + (j % (NI / 2)) * 16 + r;
+    mrow = static_cast<int>(gemm1_row(ACT, p.N_act, jj, j < NI / 2 ? 0 : 1));
+  }
+  const int64_t mbase = static_cast<int64_t>(e) * nk * p.Nout;
+  const uint16_t* ms = p.b_gscale + mbase;
+  const uint8_t* mz = p.b_zero + (mbase >> 1);
+  const int nout1 = static_cast<int>(p.Nout);
+
+  // ---- GEMM1: stages kw, kw + 4, ...; one stage of registers, reloaded
+  // piecewise as soon as each piece is consumed (scale / zero dword after its
+  // ds_bpermutes, each weight block after its MFMAs, the activations -- L2
+  // hits -- after the last MFMA), so the next stage's loads overlap this
+  // stage's arithmetic
+  const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
+  f32x4_t acc[NI];
+#pragma unroll
+  for (int j = 0; j < NI; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // one unconditional meta load per lane (lanes 40-63 re-read a zero dword)
+  auto meta_at = [&](int kt) {
+    const int mi = mrow + kt * nout1;
+    return *reinterpret_cast<const int*>(lane < 32 ? reinterpret_cast<const uint8_t*>(ms + mi) : mz + (mi >> 1));
+  };
+  {
+    int kt = kw;
+    i32x4_t av[4], wb[NI];
+    int meta = 0;
+    if (kt < nk) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) av[d] = *reinterpret_cast<const i32x4_t*>(ap + static_cast<int64_t>(kt) * 256 + 16 * d);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr0 + w_joff[j] + static_cast<int64_t>(kt) * 1024);
+      meta = meta_at(kt);
+    }
+    for (; kt < nk; kt += kFzKw) {
+      const int kn = kt + kFzKw;
+      const bool more = kn < nk;
+      unsigned sw[NI], zw[NI];
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        sw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), meta));
+        zw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), meta));
+      }
+      if (more) meta = meta_at(kn);
+      bf16x8_t a[4];
+      f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const int x01 = av[d][0], x23 = av[d][1], x45 = av[d][2], x67 = av[d][3];
+        a[d] = as_bf16x8(__builtin_amdgcn_perm(x45, x01, 0x05040100), __builtin_amdgcn_perm(x45, x01, 0x07060302),
+                         __builtin_amdgcn_perm(x67, x23, 0x05040100), __builtin_amdgcn_perm(x67, x23, 0x07060302));
+        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], ones, xs, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const unsigned wv = static_cast<unsigned>(wb[j][d]);
+          const int b0 = static_cast<int>((wv & 0x000f000fu) | 0x43004300u);
+          const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
+          const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
+          const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
+        }
+        if (more) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr0 + w_joff[j] + static_cast<int64_t>(kn) * 1024);
+        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw[j] >> 16) : (sw[j] & 0xffffu))));
+        const float z = static_cast<float>((zw[j] >> (4 * (r16 & 7))) & 15u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[r] - (128.0f + z) * xs[r]);
+      }
+      if (more) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) av[d] = *reinterpret_cast<const i32x4_t*>(ap + static_cast<int64_t>(kn) * 256 + 16 * d);
+      }
+    }
+  }
+
+  // ---- GEMM2 operands: the wave's row batches b = wid, wid + 16, ...;
+  // the first batch is requested before the GEMM1 reduction
+  const int64_t K2 = q.Nout;
+  const int64_t w2_bytes = q.Kred / 2;
+  const int n_blk = static_cast<int>(K2 / kFzBatchRows);
+  const int64_t grp = static_cast<int64_t>(e) * (q.Kred / 128) + c;  // (expert, quant group)
+  const uint8_t* B2 = q.B + static_cast<int64_t>(e) * K2 * w2_bytes + static_cast<int64_t>(c) * 1024 +
+                      (lane >> 4) * 256 + r16 * 16;
+  const uint16_t* s2 = q.b_gscale + grp * K2;
+  const uint8_t* z2 = q.b_zero + (grp * K2) / 2;
+  auto load2 = [&](int b, W2Batch& W) {
+#pragma unroll
+    for (int i = 0; i < kFzBatch; ++i)
+      W.w[i] = *reinterpret_cast<const i32x4_t*>(B2 + static_cast<int64_t>(b * kFzBatch + i) * 16 * w2_bytes);
+    // unconditional loads (surplus lanes re-read a valid dword): no branch
+    // between the batch's loads and the waits for the previous batch
+    W.sm = *reinterpret_cast<const int*>(s2 + kFzBatchRows * b + 2 * (lane % (kFzBatchRows / 2)));
+    W.zm = *reinterpret_cast<const int*>(z2 + kFzBatchRows / 2 * b + 4 * (lane % (kFzBatchRows / 8)));
+
+  };
+  W2Batch W0, W1;
+  int b = wid;
+  if (b < n_blk) load2(b, W0);
+
+  // ---- GEMM1 reduction over the 4 waves of a row block, activation -> LDS
+  if (kw > 0) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) red[kw - 1][rb][j][lane] = acc[j];
+  }
+  __syncthreads();
+  if (kw == 0) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int w = 0; w < kFzKw - 1; ++w) {
+        const f32x4_t u = red[w][rb][j][lane];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][r] += u[r];
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = (lane >> 4) * 4 + r;
+      float g = 1.0f;
+      if (m < n_rows && p.gamma) {
+        const int s = slot_of(m);
+        g = TINY ? p.tiny_w[s] : p.gate_scal[s];
+      }
+#pragma unroll
+      for (int j = 0; j < NI / 2; ++j) {
+        const uint16_t v = m < n_rows ? f32_to_bf16(gemm1_act<ACT>(p, acc[j][r], acc[j + NI / 2][r], 0.f, 0.f, g)) : 0;
+        *reinterpret_cast<uint16_t*>(&act_lds[m * kFzPitch + 2 * (rb * (BN / 2) + j * 16 + r16)]) = v;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- GEMM2: A = the tile's act slice (lane: row r16, elements 32 (lane /
+  // 16) .. + 31, permuted to the nibble pairing), shared by every batch
+  bf16x8_t a2[4];
+  f32x4_t xs2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const i32x4_t v = *reinterpret_cast<const i32x4_t*>(&act_lds[r16 * kFzPitch + (lane >> 4) * 64 + 16 * d]);
+    a2[d] = as_bf16x8(__builtin_amdgcn_perm(v[2], v[0], 0x05040100), __builtin_amdgcn_perm(v[2], v[0], 0x07060302),
+                      __builtin_amdgcn_perm(v[3], v[1], 0x05040100), __builtin_amdgcn_perm(v[3], v[1], 0x07060302));
+    xs2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[d], ones, xs2, 0, 0, 0);
+  }
+  // y stores go through a buffer descriptor over the call's planes: rows of
+  // the tile without a slot get an out-of-range offset, which the hardware
+  // drops -- no branch around the stores (a branch there makes the compiler
+  // wait for the next batch's loads before storing)
+  const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+      q.out, 0, static_cast<int>(static_cast<int64_t>(q.splits) * q.out_split_stride * 4), kBufferDword3);
+  uint32_t yoff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    yoff[r] = ys[r] >= 0 ? static_cast<uint32_t>((c * q.out_split_stride + static_cast<int64_t>(ys[r]) * K2) * 4)
+                         : 0x80000000u;
+  auto consume2 = [&](int bb, const W2Batch& W) {
+#pragma unroll
+    for (int i = 0; i < kFzBatch; ++i) {
+      f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const unsigned wv = static_cast<unsigned>(W.w[i][d]);
+        const int b0 = static_cast<int>((wv & 0x000f000fu) | 0x43004300u);
+        const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
+        const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
+        const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
+      }
+      // row 16 i + r16 of the batch: scale half r16 % 2 of lane 8 i + r16 / 2,
+      // zero nibble r16 % 8 of lane 2 i + r16 / 8
+      const unsigned sw = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * i + (r16 >> 1)), W.sm));
+      const unsigned zw = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (2 * i + (r16 >> 3)), W.zm));
+      const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw >> 16) : (sw & 0xffffu))));
+      const float z = static_cast<float>((zw >> (4 * (r16 & 7))) & 15u);
+      const int64_t col = static_cast<int64_t>(bb) * kFzBatchRows + i * 16 + r16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sc * (t[r] - (128.0f + z) * xs2[r]) * yg[r]), yr,
+                                              static_cast<int>(yoff[r] + 4 * static_cast<uint32_t>(col)), 0, 0);
+    }
+  };
+  while (b < n_blk) {
+    const int b1 = b + kFzWaves;
+    if (b1 < n_blk) load2(b1, W1);
+    consume2(b, W0);
+    if (b1 >= n_blk) break;
+    const int b2 = b1 + kFzWaves;
+    if (b2 < n_blk) load2(b2, W0);
+    consume2(b1, W1);
+    b = b2;
+  }
+}
+
+
 }  // namespace decode
 
 // Row blocks per workgroup by format and GEMM (build-time overridable for
@@ -888,6 +1184,27 @@ constexpr int kRsMinTiles = 14;
 // max_tiles expert tiles, 0 when the row-block kernel runs
 int decode_int4_row_split(int64_t max_tiles) {
   return FMOE_DECODE_INT4_RS != 0 && max_tiles >= kRsMinTiles ? decode::kRsBlocks : 0;
+}
+
+// One launch of fused_int4_kernel: p = GEMM1 (x, w13, routing: tile map or
+// the tiny-batch top-k ids), q = GEMM2 (w2, gammas, bias, y planes).
+int launch_fused_int4(const GemmParams& p, const GemmParams& q, hipStream_t s) {
+  if (p.max_tiles <= 0) return FMOE_OK;
+  if (p.N_act % decode::kFzCols != 0 || q.Nout % 128 != 0 || p.act == kActSwiglu || p.bias || q.bias ||
+      q.splits != p.N_act / decode::kFzCols || static_cast<int64_t>(q.splits) * q.out_split_stride * 4 >= (int64_t(1) << 31))
+    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED,
+                           "fused int4 decode: N %% 128, K %% 128, SiLU / GELU, no bias, N / 128 planes < 2 GiB");
+  const dim3 g(static_cast<unsigned>(p.N_act / decode::kFzCols), static_cast<unsigned>(p.max_tiles));
+  const dim3 b(decode::kFzThreads);
+  const bool tiny = p.tiny_ids != nullptr;
+  if (p.act == kActGelu) {
+    if (tiny) decode::fused_int4_kernel<kActGelu, true><<<g, b, 0, s>>>(p, q);
+    else decode::fused_int4_kernel<kActGelu, false><<<g, b, 0, s>>>(p, q);
+  } else {
+    if (tiny) decode::fused_int4_kernel<kActSilu, true><<<g, b, 0, s>>>(p, q);
+    else decode::fused_int4_kernel<kActSilu, false><<<g, b, 0, s>>>(p, q);
+  }
+  return fmoe_host::check_launch("fused_int4");
 }
 
 int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {

@@ -139,6 +139,76 @@ inline void sum_launch_dims(int64_t K, int64_t M, dim3& g, dim3& b) {
   b = dim3(static_cast<unsigned>(threads));
 }
 
+// Top-k combine over many split planes (the one-launch int4 decode writes
+// N / 128 of them): out[t, c] = bf16(scale * sum_g S_g), g = 0..15 in order,
+// S_g = the sum over the token's slots j (ascending) and, within a slot, its
+// planes p = g, g + 16, ... (ascending) -- a fixed order, so every run is
+// bit-identical.  A workgroup = one token x 64 columns: thread (g, quad)
+// accumulates its S_g for 4 columns, the 16 partial sums meet in LDS.
+// Slots: gate_indx (< 0: dropped) or, with gate_indx null, flat slots t k + j
+// whose expert id is in [0, n_experts).
+constexpr int kPlaneGroups = 16;
+__global__ __launch_bounds__(256) void moe_sum_planes_kernel(const float* __restrict__ y, int planes,
+                                                             int64_t plane_stride,
+                                                             const int32_t* __restrict__ gate_indx,
+                                                             const int32_t* __restrict__ ids, int n_experts,
+                                                             int k, int64_t K, float scale,
+                                                             uint16_t* __restrict__ out) {
+  __shared__ int rows[32];
+  __shared__ float4 part[kPlaneGroups][16];
+  const int tid = threadIdx.x, quad = tid & 15, g = tid >> 4;
+  const int64_t t = blockIdx.y;
+  const int64_t c = static_cast<int64_t>(blockIdx.x) * 64 + quad * 4;
+  if (tid < k) {
+    const int64_t f = t * k + tid;
+    int sl;
+    if (gate_indx) {
+      sl = gate_indx[f];
+    } else {
+      const int id = ids[f];
+      sl = id >= 0 && id < n_experts ? static_cast<int>(f) : -1;
+    }
+    rows[tid] = sl;
+  }
+  __syncthreads();
+  const int per = (planes - g + kPlaneGroups - 1) / kPlaneGroups;  // planes of group g
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < k; ++j) {
+    const int row = rows[j];
+    if (row < 0) continue;
+    const float* src = y + static_cast<int64_t>(row) * K + c + static_cast<int64_t>(g) * plane_stride;
+    for (int i0 = 0; i0 < per; i0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (i0 + u < per)
+          v[u] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(i0 + u) * kPlaneGroups * plane_stride);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (i0 + u < per) {
+          acc.x += v[u].x;
+          acc.y += v[u].y;
+          acc.z += v[u].z;
+          acc.w += v[u].w;
+        }
+    }
+  }
+  part[g][quad] = acc;
+  __syncthreads();
+  if (g != 0) return;
+  float4 sum = part[0][quad];
+  for (int h = 1; h < kPlaneGroups; ++h) {
+    const float4 v = part[h][quad];
+    sum.x += v.x;
+    sum.y += v.y;
+    sum.z += v.z;
+    sum.w += v.w;
+  }
+  const uint32_t w0 = f32_to_bf16(sum.x * scale) | (static_cast<uint32_t>(f32_to_bf16(sum.y * scale)) << 16);
+  const uint32_t w1 = f32_to_bf16(sum.z * scale) | (static_cast<uint32_t>(f32_to_bf16(sum.w * scale)) << 16);
+  *reinterpret_cast<uint2*>(out + t * K + c) = make_uint2(w0, w1);
+}
+
 }  // namespace fmoe
 
 using namespace fmoe;
@@ -203,5 +273,16 @@ int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, 
   moe_sum_kernel<__bf16, 8><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
                                          nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
+}
+// moe_sum over the N / 128 planes of the one-launch int4 decode (gate_indx,
+// or flat slots checked against the expert ids when gate_indx is null).
+int moe_sum_planes(const float* y, int planes, const int32_t* gate_indx, const int32_t* ids, int E,
+                   int64_t M, int k, int64_t K, float scale, void* out, hipStream_t s) {
+  if (k > 32 || K % 64 != 0 || M > 65535)
+    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "moe_sum_planes: k <= 32, K %% 64 == 0, M <= 65535");
+  const dim3 g(static_cast<unsigned>(K / 64), static_cast<unsigned>(M)), b(256);
+  moe_sum_planes_kernel<<<g, b, 0, s>>>(y, planes, M * k * K, gate_indx, ids, E, k, K, scale,
+                                        static_cast<uint16_t*>(out));
+  return check_launch("moe_sum_planes");
 }
 }  // namespace fmoe

@@ -73,3 +73,10 @@ def test_argument_errors_map_to_reference_convention():
     fa.K = 128
     assert L.fmoe_fused_experts_workspace_bytes(ctypes.byref(fa)) > 0
     assert L.fmoe_fused_experts(ctypes.byref(fa), None) == _lib.FMOE_ERR_INVALID  # null pointers
+    # int4 weights take SiLU / GELU only (no SWIGLU row pairing)
+    fa.wtype, fa.group_size, fa.activation = _lib.W_INT4_TILED, 128, _lib.ACT_SWIGLU
+    assert L.fmoe_fused_experts_workspace_bytes(ctypes.byref(fa)) == 0
+    assert L.fmoe_fused_experts(ctypes.byref(fa), None) == _lib.FMOE_ERR_UNSUPPORTED
+    assert b"SWIGLU" in L.fmoe_last_error()
+    fa.activation = _lib.ACT_SILU
+    assert L.fmoe_fused_experts_workspace_bytes(ctypes.byref(fa)) > 0
