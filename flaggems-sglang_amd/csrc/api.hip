@@ -15,6 +15,7 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s);
 int launch_fused_int4(const GemmParams& p, const GemmParams& q, hipStream_t s);
+bool fused_int4_fits(int64_t slots, int64_t K);
 int moe_sum_planes(const float* y, int planes, const int32_t* gate_indx, const int32_t* ids, int E,
                    int64_t M, int k, int64_t K, float scale, void* out, hipStream_t s);
 }  // namespace fmoe
@@ -374,7 +375,7 @@ int check_fused(const fmoe_fused_args* a) {
 #endif
 bool fused_int4_route(const fmoe_fused_args* a, int bm) {
   return a->wtype == FMOE_W_INT4_TILED && bm == kDecodeBM && a->activation != FMOE_ACT_SWIGLU &&
-         a->M <= FMOE_FUSED_INT4_MAX_M && a->top_k <= 32;
+         a->M <= FMOE_FUSED_INT4_MAX_M && a->top_k <= 32 && fused_int4_fits(a->M * a->top_k, a->K);
 }
 
 FusedLayout layout(const fmoe_fused_args* a) {

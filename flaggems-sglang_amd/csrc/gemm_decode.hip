@@ -869,6 +869,8 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
 // at or past num_records are dropped by the hardware
 constexpr int kBufferDword3 = 0x00020000;
 constexpr int kFzWaves = 16;
+constexpr int kFzXBytes = 48 * 1024;  // LDS for the tile's x rows, later the partial sums
+static_assert((kWaves - 1) * 4 * NI * kWave * 16 <= kFzXBytes, "partial sums fit the x staging LDS");
 constexpr int kFzThreads = kFzWaves * kWave;
 constexpr int kFzCols = 128;                      // act columns per workgroup
 constexpr int kFzRowBlocks = kFzCols / (BN / 2);  // GEMM1 64-row blocks per workgroup
@@ -893,7 +895,9 @@ struct W2Batch {
 template <int ACT, bool TINY>
 __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p, GemmParams q) {
   static_assert(ACT != kActSwiglu, "int4 decode: SiLU / GELU row layout only");
-  __shared__ f32x4_t red[kFzKw - 1][kFzRowBlocks][NI][kWave];
+  // x rows of the tile during GEMM1, then the cross-wave partial sums
+  __shared__ __attribute__((aligned(16))) uint8_t xr_lds[kFzXBytes];
+  auto red = reinterpret_cast<f32x4_t (*)[kFzRowBlocks][NI][kWave]>(xr_lds);
   __shared__ __attribute__((aligned(16))) uint8_t act_lds[BM * kFzPitch];
   __shared__ TinyLds tiny_lds[1];
   const int tid = threadIdx.x, lane = tid % kWave;
@@ -915,23 +919,23 @@ __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p,
   }
   auto slot_of = [&](int r) { return TINY ? tiny_lds[0].rows[r] : row_beg + r; };
   const int r16 = lane & 15;
-  // GEMM2 output slots of this lane (tile rows 4 (lane / 16) + r) and their
-  // gammas, loaded here so that they have long arrived when the GEMM2 loop
-  // (whose waits must not cover them) stores
-  int ys[4];
-  float yg[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int m = (lane >> 4) * 4 + r;
-    ys[r] = m < n_rows ? slot_of(m) : -1;
-    yg[r] = (ys[r] >= 0 && q.gamma) ? (TINY ? q.tiny_w[ys[r]] : q.gate_scal[ys[r]]) : 1.0f;
-  }
 
   // ---- GEMM1 addresses (the row-block kernel's, 64-row block nt)
   const int nt = c * kFzRowBlocks + rb;
-  const int s_a = slot_of(r16 < n_rows ? r16 : 0);
-  const int64_t a_row = (TINY ? s_a : p.topk_indx[s_a]) / p.top_k;
-  const uint8_t* ap = p.A + a_row * p.Kred * 2 + (lane >> 4) * 64;
+  // the tile's x rows are staged in LDS once (n_rows K 2 <= kFzXBytes, which
+  // the host guarantees): GEMM1 then issues only weight and scale loads
+  {
+    const int vr = static_cast<int>(p.Kred / 8);  // 16-byte pieces per row
+    for (int i = tid; i < n_rows * vr; i += kFzThreads) {
+      const int m = i / vr, v = i - m * vr;
+      const int sm = slot_of(m);
+      const int64_t xrow = (TINY ? sm : p.topk_indx[sm]) / p.top_k;
+      *reinterpret_cast<i32x4_t*>(&xr_lds[(static_cast<int64_t>(m) * vr + v) * 16]) =
+          *reinterpret_cast<const i32x4_t*>(p.A + (xrow * vr + v) * 16);
+    }
+  }
+  __syncthreads();
+  const int a_off = (r16 < n_rows ? r16 : 0) * static_cast<int>(p.Kred) * 2 + (lane >> 4) * 64;
   const int64_t w_bytes = p.Kred / 2;
   const int nk = static_cast<int>(p.Kred / 128);
   const uint8_t* Be = p.B + static_cast<int64_t>(e) * p.Nout * w_bytes;
@@ -978,7 +982,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p,
     int meta = 0;
     if (kt < nk) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) av[d] = *reinterpret_cast<const i32x4_t*>(ap + static_cast<int64_t>(kt) * 256 + 16 * d);
+      for (int d = 0; d < 4; ++d) av[d] = *reinterpret_cast<const i32x4_t*>(&xr_lds[a_off + kt * 256 + 16 * d]);
 #pragma unroll
       for (int j = 0; j < NI; ++j) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr0 + w_joff[j] + static_cast<int64_t>(kt) * 1024);
       meta = meta_at(kt);
@@ -1022,7 +1026,7 @@ __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p,
       }
       if (more) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) av[d] = *reinterpret_cast<const i32x4_t*>(ap + static_cast<int64_t>(kn) * 256 + 16 * d);
+        for (int d = 0; d < 4; ++d) av[d] = *reinterpret_cast<const i32x4_t*>(&xr_lds[a_off + kn * 256 + 16 * d]);
       }
     }
   }
@@ -1051,7 +1055,20 @@ __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p,
   int b = wid;
   if (b < n_blk) load2(b, W0);
 
+  // GEMM2 output slots of this lane (tile rows 4 (lane / 16) + r) and their
+  // gammas, loaded before the barriers below, which wait for them: the GEMM2
+  // loop's waits then need not cover them
+  int ys[4];
+  float yg[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = (lane >> 4) * 4 + r;
+    ys[r] = m < n_rows ? slot_of(m) : -1;
+    yg[r] = (ys[r] >= 0 && q.gamma) ? (TINY ? q.tiny_w[ys[r]] : q.gate_scal[ys[r]]) : 1.0f;
+  }
+
   // ---- GEMM1 reduction over the 4 waves of a row block, activation -> LDS
+  __syncthreads();  // every wave has read its last x stage: the LDS takes the partial sums
   if (kw > 0) {
 #pragma unroll
     for (int j = 0; j < NI; ++j) red[kw - 1][rb][j][lane] = acc[j];
@@ -1186,14 +1203,22 @@ int decode_int4_row_split(int64_t max_tiles) {
   return FMOE_DECODE_INT4_RS != 0 && max_tiles >= kRsMinTiles ? decode::kRsBlocks : 0;
 }
 
+// Whether a call with `slots` top-k slots and hidden size K fits the one-launch
+// int4 kernel's LDS staging of a tile's x rows (at most min(16, slots) rows).
+bool fused_int4_fits(int64_t slots, int64_t K) {
+  const int64_t rows = slots < decode::BM ? slots : decode::BM;
+  return rows * K * 2 <= decode::kFzXBytes;
+}
+
 // One launch of fused_int4_kernel: p = GEMM1 (x, w13, routing: tile map or
 // the tiny-batch top-k ids), q = GEMM2 (w2, gammas, bias, y planes).
 int launch_fused_int4(const GemmParams& p, const GemmParams& q, hipStream_t s) {
   if (p.max_tiles <= 0) return FMOE_OK;
   if (p.N_act % decode::kFzCols != 0 || q.Nout % 128 != 0 || p.act == kActSwiglu || p.bias || q.bias ||
-      q.splits != p.N_act / decode::kFzCols || static_cast<int64_t>(q.splits) * q.out_split_stride * 4 >= (int64_t(1) << 31))
+      q.splits != p.N_act / decode::kFzCols || static_cast<int64_t>(q.splits) * q.out_split_stride * 4 >= (int64_t(1) << 31) ||
+      !fused_int4_fits(q.out_split_stride / q.Nout, p.Kred))
     return fmoe_host::fail(FMOE_ERR_UNSUPPORTED,
-                           "fused int4 decode: N %% 128, K %% 128, SiLU / GELU, no bias, N / 128 planes < 2 GiB");
+                           "fused int4 decode: N %% 128, K %% 128, SiLU / GELU, no bias, N / 128 planes < 2 GiB, x rows in LDS");
   const dim3 g(static_cast<unsigned>(p.N_act / decode::kFzCols), static_cast<unsigned>(p.max_tiles));
   const dim3 b(decode::kFzThreads);
   const bool tiny = p.tiny_ids != nullptr;
