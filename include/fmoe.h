@@ -62,7 +62,8 @@ enum fmoe_activation {
   FMOE_ACT_SILU = 0,   /* silu(gate) * up, gate rows 0..N-1, up rows N..2N-1 (ops/fused_moe.py:28-47) */
   FMOE_ACT_GELU = 1,   /* gelu(gate) * up with the exact (erf) GELU, same split (ops/fused_moe.py:203-204) */
   FMOE_ACT_SWIGLU = 2, /* swiglu of the bias path (ops/fused_moe.py:258-259): rows interleaved,
-                          gate = row 2j, linear = row 2j+1; see fmoe_epilogue */
+                          gate = row 2j, linear = row 2j+1; see fmoe_epilogue.  Not with int4
+                          weights (FMOE_ERR_UNSUPPORTED) */
 };
 
 /* Text of a status code, and the message of the last failure on this thread. */
