@@ -131,7 +131,9 @@ __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restri
 }
 
 // Small calls (decode) use 64-thread blocks, so their few workgroups spread
-// over more CUs (each CU keeps only so many loads in flight).
+// over more CUs (each CU keeps only so many loads in flight); they also take
+// all of a token's terms in one batch (k * splits <= 32).  Large calls keep
+// 8-term batches: the 32-term batch's registers cost occupancy there.
 inline void sum_launch_dims(int64_t K, int64_t M, dim3& g, dim3& b) {
   const int64_t vecs = K / 4;
   const int threads = vecs * M < 64 * 1024 ? 64 : kSumThreads;
@@ -242,7 +244,7 @@ extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
-  if (k * splits <= 32)
+  if (k * splits <= 32 && b.x < kSumThreads)
     moe_sum_kernel<float, 32><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
         y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   else
@@ -257,7 +259,7 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
                  float scale, void* out, hipStream_t s) {
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
-  if (k * splits <= 32)
+  if (k * splits <= 32 && b.x < kSumThreads)
     moe_sum_kernel<float, 32><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
                                               static_cast<uint16_t*>(out));
   else
