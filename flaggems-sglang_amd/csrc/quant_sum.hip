@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
 // at a time: first every term's slot (the gate_indx loads together), then
 // every term's row load -- dropped slots read a row that exists and is not
 // added -- so the loads of a batch are in flight together; then the adds in
-// order.  Small calls (k * splits <= 32, decode) take all terms in one batch.
+// order.  (Large calls; decode-size calls go to moe_sum_planes_kernel.)
 constexpr int kSumThreads = 256;
 
 template <typename YT>
@@ -131,9 +131,8 @@ __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restri
 }
 
 // Small calls (decode) use 64-thread blocks, so their few workgroups spread
-// over more CUs (each CU keeps only so many loads in flight); they also take
-// all of a token's terms in one batch (k * splits <= 32).  Large calls keep
-// 8-term batches: the 32-term batch's registers cost occupancy there.
+// over more CUs (each CU keeps only so many loads in flight); most of them go
+// to moe_sum_planes_kernel instead (small_sum).
 inline void sum_launch_dims(int64_t K, int64_t M, dim3& g, dim3& b) {
   const int64_t vecs = K / 4;
   const int threads = vecs * M < 64 * 1024 ? 64 : kSumThreads;
@@ -141,14 +140,16 @@ inline void sum_launch_dims(int64_t K, int64_t M, dim3& g, dim3& b) {
   b = dim3(static_cast<unsigned>(threads));
 }
 
-// Top-k combine over many split planes (the one-launch int4 decode writes
-// N / 128 of them): out[t, c] = bf16(scale * sum_g S_g), g = 0..15 in order,
-// S_g = the sum over the token's slots j (ascending) and, within a slot, its
-// planes p = g, g + 16, ... (ascending) -- a fixed order, so every run is
-// bit-identical.  A workgroup = one token x 64 columns: thread (g, quad)
-// accumulates its S_g for 4 columns, the 16 partial sums meet in LDS.
-// Slots: gate_indx (< 0: dropped) or, with gate_indx null, flat slots t k + j
-// whose expert id is in [0, n_experts).
+// Top-k combine of small calls (decode) and of the one-launch int4 decode's
+// N / 128 planes: the terms of an output element, (slot j, plane p), are
+// split over 16 term groups g -- planes p = g, g + 16, ... of every slot when
+// there are >= 16 planes, else terms q = j * planes + p = g, g + 16, ... --
+// each group summed in ascending q, and the 16 group sums are added in order
+// g = 0..15: a fixed order per shape, so every run is bit-identical.  A
+// workgroup = one token x 64 columns: thread (g, quad) loads its terms for 4
+// columns 8 at a time (all in flight together), the group sums meet in LDS.  Slots:
+// gate_indx (< 0: dropped) or, with gate_indx null, flat slots t k + j whose
+// expert id is in [0, n_experts).
 constexpr int kPlaneGroups = 16;
 __global__ __launch_bounds__(256) void moe_sum_planes_kernel(const float* __restrict__ y, int planes,
                                                              int64_t plane_stride,
@@ -173,26 +174,57 @@ __global__ __launch_bounds__(256) void moe_sum_planes_kernel(const float* __rest
     rows[tid] = sl;
   }
   __syncthreads();
-  const int per = (planes - g + kPlaneGroups - 1) / kPlaneGroups;  // planes of group g
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int j = 0; j < k; ++j) {
-    const int row = rows[j];
-    if (row < 0) continue;
-    const float* src = y + static_cast<int64_t>(row) * K + c + static_cast<int64_t>(g) * plane_stride;
-    for (int i0 = 0; i0 < per; i0 += 8) {
+  auto add = [&](const float4& v) {
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  };
+  if (planes >= kPlaneGroups) {
+    // many planes (one-launch int4 decode): slot by slot, group g taking
+    // planes g, g + 16, ... -- q = j * planes + p order within the group
+    const int per = (planes - g + kPlaneGroups - 1) / kPlaneGroups;
+    for (int j = 0; j < k; ++j) {
+      const int row = rows[j];
+      if (row < 0) continue;
+      const float* src = y + static_cast<int64_t>(row) * K + c + static_cast<int64_t>(g) * plane_stride;
+      for (int i0 = 0; i0 < per; i0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i0 + u < per)
+            v[u] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(i0 + u) * kPlaneGroups * plane_stride);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i0 + u < per) add(v[u]);
+      }
+    }
+  } else {
+    // few planes (split-K of the decode GEMM2): the k x planes terms dealt
+    // round robin over the 16 groups, 8 loads in flight per thread
+    const int n_terms = k * planes;
+    int tj = g / planes, tp = g - tj * planes;  // (j, p) of term q, stepped without a division
+    for (int q0 = g; q0 < n_terms; q0 += 8 * kPlaneGroups) {
       float4 v[8];
+      bool ok[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (i0 + u < per)
-          v[u] = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(i0 + u) * kPlaneGroups * plane_stride);
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (i0 + u < per) {
-          acc.x += v[u].x;
-          acc.y += v[u].y;
-          acc.z += v[u].z;
-          acc.w += v[u].w;
+      for (int u = 0; u < 8; ++u) {
+        const int q = q0 + u * kPlaneGroups;
+        ok[u] = false;
+        if (q < n_terms) {
+          const int row = rows[tj];
+          if (row >= 0) {
+            v[u] = *reinterpret_cast<const float4*>(y + static_cast<int64_t>(tp) * plane_stride +
+                                                    static_cast<int64_t>(row) * K + c);
+            ok[u] = true;
+          }
+          for (tp += kPlaneGroups; tp >= planes; tp -= planes) ++tj;
         }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (ok[u]) add(v[u]);
     }
   }
   part[g][quad] = acc;
@@ -236,20 +268,29 @@ extern "C" int fmoe_quant_fp8_group(const void* x, int64_t M, int64_t K, int gro
   return check_launch("quant_fp8_group");
 }
 
+namespace fmoe {
+int moe_sum_planes(const float* y, int planes, const int32_t* gate_indx, const int32_t* ids, int E,
+                   int64_t M, int k, int64_t K, float scale, void* out, hipStream_t s);
+// Small calls (decode: fewer than 64K column quads) take the term-parallel
+// kernel: their few tokens leave most CUs idle and the per-thread term loop's
+// round trips would set the time (reference sweep M=1: 48 terms per element).
+bool small_sum(int64_t K, int64_t M, int k) {
+  return K % 64 == 0 && k <= 32 && M <= 65535 && (K / 4) * M < 64 * 1024;
+}
+}  // namespace fmoe
+
 extern "C" int fmoe_moe_sum(const float* y, int splits, const int32_t* gate_indx, int64_t M, int k,
                             int64_t K, float scale, void* out, void* stream) {
   if (M < 0 || k < 1 || K <= 0 || K % 4 != 0 || splits < 1)
     return fail(FMOE_ERR_INVALID, "moe_sum: need K %% 4 == 0, k >= 1, splits >= 1");
   if (M == 0) return FMOE_OK;
   if (!y || !gate_indx || !out) return fail(FMOE_ERR_INVALID, "moe_sum: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (small_sum(K, M, k)) return moe_sum_planes(y, splits, gate_indx, nullptr, 0, M, k, K, scale, out, s);
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
-  if (k * splits <= 32 && b.x < kSumThreads)
-    moe_sum_kernel<float, 32><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
-        y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
-  else
-    moe_sum_kernel<float, 8><<<g, b, 0, static_cast<hipStream_t>(stream)>>>(
-        y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
+  moe_sum_kernel<float, 8><<<g, b, 0, s>>>(y, splits, M * k * K, gate_indx, nullptr, 0, M, k, K, scale,
+                                           static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 
@@ -257,14 +298,11 @@ namespace fmoe {
 // moe_sum of the tiny-batch decode path: y rows are flat slots (t * k + j).
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
+  if (small_sum(K, M, k)) return moe_sum_planes(y, splits, nullptr, ids, E, M, k, K, scale, out, s);
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
-  if (k * splits <= 32 && b.x < kSumThreads)
-    moe_sum_kernel<float, 32><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
-                                              static_cast<uint16_t*>(out));
-  else
-    moe_sum_kernel<float, 8><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
-                                             static_cast<uint16_t*>(out));
+  moe_sum_kernel<float, 8><<<g, b, 0, s>>>(y, splits, M * k * K, nullptr, ids, E, M, k, K, scale,
+                                           static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
 // moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
@@ -276,8 +314,8 @@ int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, 
                                          nullptr, 0, M, k, K, scale, static_cast<uint16_t*>(out));
   return check_launch("moe_sum");
 }
-// moe_sum over the N / 128 planes of the one-launch int4 decode (gate_indx,
-// or flat slots checked against the expert ids when gate_indx is null).
+// moe_sum_planes_kernel over `planes` split planes (gate_indx, or flat slots
+// checked against the expert ids when gate_indx is null).
 int moe_sum_planes(const float* y, int planes, const int32_t* gate_indx, const int32_t* ids, int E,
                    int64_t M, int k, int64_t K, float scale, void* out, hipStream_t s) {
   if (k > 32 || K % 64 != 0 || M > 65535)
