@@ -5,7 +5,9 @@ FUSED_MOE_SHAPES entry, plus apply_router_weight_on_input on the small
 shapes; inputs per its _make_inputs, seed M+K+N+E+topk) and adds the
 BASELINE configurations (bf16, skewed routing, fp8 block-scale, int4) at
 sizes the oracle finishes in seconds.  Tolerances: bf16 atol=rtol=2e-2;
-fp8 / int4 5e-2 against the dequantize-then-compute oracle.
+fp8 / int4 5e-2 against the dequantize-then-compute oracle -- with the
+absolute term scaled by the output RMS (_close), and on the BASELINE input
+recipes also exactly as written (_close_literal).
 """
 
 import numpy as np
@@ -55,6 +57,16 @@ def _close(out, ref, tol):
     if ref.numel():
         rel = float((out - ref).norm() / ref.norm().clamp_min(1e-30))
         assert rel < tol / 4, f"global relative error {rel:.3e}"
+
+
+def _close_literal(out, ref, tol):
+    """north_star's tolerance as written: |out - ref| <= tol + tol * |ref|
+    elementwise (torch.testing.assert_close(atol=rtol=tol)).  Used on the
+    BASELINE input recipes (weights N(0, 0.02), outputs of RMS ~1), where
+    one bf16 ulp of the output is well inside tol; the reference's own test
+    shapes (weights N(0,1)*0.1, output RMS ~10, where an output ulp alone is
+    0.06) take _close."""
+    torch.testing.assert_close(out.float().cpu(), ref.float(), atol=tol, rtol=tol)
 
 
 @pytest.mark.parametrize("shape", FUSED_MOE_SHAPES_SMALL + FUSED_MOE_SHAPES_LARGE,
@@ -122,6 +134,7 @@ def _bf16_case(M, K, N, E, k, bias=0.0, seed=None):
                                         d["topk_weights"].to(DEV), d["topk_ids"].to(DEV))
     ref = O.fused_experts(d["x"], d["w13"], d["w2"], d["topk_weights"], d["topk_ids"])
     _close(out, ref, 2e-2)
+    _close_literal(out, ref, 2e-2)
 
 
 @pytest.mark.parametrize("M", [1, 16, 256])
@@ -152,6 +165,7 @@ def test_dsv3_fp8(M):
     ref = O.fused_experts_fp8(d["x"], q1.cpu(), s1.cpu(), q2.cpu(), s2.cpu(), d["topk_weights"],
                               d["topk_ids"])
     _close(out, ref, 5e-2)
+    _close_literal(out, ref, 5e-2)
 
 
 @pytest.mark.parametrize("K,N", [(7168, 256), (8448, 256), (256, 8448)])
@@ -213,6 +227,7 @@ def test_mixtral_w4a16(M):
     ref = O.fused_experts_w4a16(d["x"], q1.cpu(), sc1.cpu(), z1.cpu(), q2.cpu(), sc2.cpu(),
                                 z2.cpu(), d["topk_weights"], d["topk_ids"])
     _close(out, ref, 5e-2)
+    _close_literal(out, ref, 5e-2)
 
 
 def test_product_quantizers_match_oracle():
