@@ -361,11 +361,11 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   // per-lane fragment offsets within a 16-row block's units
   const int foff0 = frag_off<SB>(lane, lane >> 4);
   const int foff1 = SB == 64 ? 0 : frag_off<SB>(lane, 4 + (lane >> 4));
-  // bf16: the wave raises its issue priority for its fragment reads and
-  // MFMAs and drops it before the next stage's wait and DMA issue (Mixtral
-  // M=4096 GEMM1 1.90 -> 1.86 ms, Qwen3 M=8192 GEMM1 -1%; fp8 GEMM1 +3.6%,
-  // so fp8 keeps one level)
-  constexpr int kPrio = FP8 ? 0 : 1;
+  // The wave raises its issue priority for its fragment reads and MFMAs and
+  // drops it before the next stage's wait and DMA issue: bf16 (Mixtral
+  // M=4096 GEMM1 1.90 -> 1.86 ms, Qwen3 M=8192 GEMM1 -1%) and fp8 GEMM2
+  // (DSV3 M=4096 -1.3%); fp8 GEMM1 keeps one level (+3.6% with it)
+  constexpr int kPrio = (FP8 && MODE == Mode::kGemm1Silu) ? 0 : 1;
   auto compute = [&](int kt) {
     if (kPrio) __builtin_amdgcn_s_setprio(kPrio);
     const uint8_t* st = lds[kt % NBUF];
