@@ -130,6 +130,70 @@ __global__ __launch_bounds__(kSumThreads) void moe_sum_kernel(const YT* __restri
   }
 }
 
+// Top-k sum of one plane of bf16 rows (prefill GEMM2 without split-K, the
+// fused path): one wave per token, lane l owning 8-column chunks l, l + 64,
+// ...; for each pair of chunks the rows of up to 8 terms are all requested
+// (16-byte loads) before the adds, which run in term order j = 0..k-1 per
+// column -- moe_sum_kernel's order, so results are bit-identical.  Slots come
+// from gate_indx (< 0: dropped, a valid row is read and not added).  k <= 64.
+__global__ __launch_bounds__(256) void moe_sum_rows_bf16_kernel(const uint16_t* __restrict__ y,
+                                                                const int32_t* __restrict__ gate_indx,
+                                                                int64_t n_tok, int k, int64_t K,
+                                                                float scale, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (t >= n_tok) return;
+  const int64_t nchunk = K / 8;
+  const int my = lane < k ? gate_indx[t * k + lane] : -1;
+  for (int64_t c0 = lane; c0 < nchunk; c0 += 2 * kWave) {
+    float acc[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+    const bool c1 = c0 + kWave < nchunk;
+    for (int j0 = 0; j0 < k; j0 += 8) {
+      i32x4_t v[2][8];
+      bool ok[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u;
+        const int row = __shfl(my, j < k ? j : 0, kWave);
+        ok[u] = j < k && row >= 0;
+        const uint16_t* src = y + static_cast<int64_t>(row >= 0 ? row : 0) * K + c0 * 8;
+        if (j < k) {
+          v[0][u] = *reinterpret_cast<const i32x4_t*>(src);
+          if (c1) v[1][u] = *reinterpret_cast<const i32x4_t*>(src + kWave * 8);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (!ok[u]) continue;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (h == 1 && !c1) continue;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t w = static_cast<uint32_t>(v[h][u][q]);
+            acc[h][2 * q] += __uint_as_float(w << 16);
+            acc[h][2 * q + 1] += __uint_as_float(w & 0xffff0000u);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (h == 1 && !c1) continue;
+      i32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = static_cast<int>(f32_to_bf16(acc[h][2 * q] * scale) |
+                                (static_cast<uint32_t>(f32_to_bf16(acc[h][2 * q + 1] * scale)) << 16));
+      *reinterpret_cast<i32x4_t*>(out + t * K + (c0 + h * kWave) * 8) = o;
+    }
+  }
+}
+
 // Small calls (decode) use 64-thread blocks, so their few workgroups spread
 // over more CUs (each CU keeps only so many loads in flight); most of them go
 // to moe_sum_planes_kernel instead (small_sum).
@@ -308,6 +372,14 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
 // moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
+#ifndef FMOE_SUM_ROWS
+#define FMOE_SUM_ROWS 1
+#endif
+  if (FMOE_SUM_ROWS && k <= kWave && K % 8 == 0) {
+    const dim3 g(static_cast<unsigned>((M + 3) / 4)), b(256);
+    moe_sum_rows_bf16_kernel<<<g, b, 0, s>>>(y, gate_indx, M, k, K, scale, static_cast<uint16_t*>(out));
+    return check_launch("moe_sum_rows");
+  }
   dim3 g, b;
   sum_launch_dims(K, M, g, b);
   moe_sum_kernel<__bf16, 8><<<g, b, 0, s>>>(reinterpret_cast<const __bf16*>(y), 1, M * k * K, gate_indx,
