@@ -141,7 +141,15 @@ extern "C" int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_rou
     if (wgs >= kPrefillNoSplitWgs) return 1;
     const int64_t stage_elems = wtype == FMOE_W_BF16 ? 32 : 128;
     int64_t sp = (kPrefillTargetWgs + wgs - 1) / (wgs > 0 ? wgs : 1);
-    const int64_t max_sp = N / stage_elems / 16 > 1 ? N / stage_elems / 16 : 1;  // >= 16 stages each
+    // each split keeps >= 64 stages: a short reduction gains less from the
+    // split than its extra prologue / epilogue and fp32 planes cost (reference
+    // sweep M=1024 / 2048, 48 stages: unsplit 549 -> 504 / 854 -> 738 us;
+    // Mixtral M=4096, 224 stages, keeps its 3 splits)
+#ifndef FMOE_PREFILL_MIN_SPLIT_STAGES
+#define FMOE_PREFILL_MIN_SPLIT_STAGES 64
+#endif
+    constexpr int64_t kMinStages = FMOE_PREFILL_MIN_SPLIT_STAGES;
+    const int64_t max_sp = N / stage_elems / kMinStages > 1 ? N / stage_elems / kMinStages : 1;
     if (sp > max_sp) sp = max_sp;
     if (sp > 4) sp = 4;
     return static_cast<int>(sp < 1 ? 1 : sp);
