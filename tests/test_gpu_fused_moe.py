@@ -378,9 +378,10 @@ def test_fp8_fused_act_quant_matches_stage_path(M, on_input):
     """The fused fp8 prefill path quantizes the GEMM1 activation in the GEMM1
     epilogue; the stage path (triton_kernel_fused_experts) runs the separate
     fmoe_quant_fp8_group pass on the bf16 activation.  With N large enough
-    that GEMM2 splits K (fp32 partial planes in both paths) the two must agree
-    bit for bit."""
-    K, N, E, k = 512, 4096, 8, 2
+    that GEMM2 splits K (fp32 partial planes in both paths; a split needs >= 64
+    stages of 128 on each side, so N >= 16384) the two must agree bit for
+    bit."""
+    K, N, E, k = 512, 16384, 8, 2
     d = O.make_inputs(M, K, N, E, k, wscale=0.02)
     q1, s1 = Q.quantize_fp8_block(d["w13"].to(DEV))
     q2, s2 = Q.quantize_fp8_block(d["w2"].to(DEV))
