@@ -7,14 +7,16 @@
 //   rows    per token: order its k ids ascending (rank by counting, ties by
 //           column), write expt_indx / expt_scal, count the chunk's per-expert
 //           histogram in LDS;
-//   scan    one workgroup: per expert, exclusive prefix over chunks, then the
-//           exclusive scan over experts (token_offs_raw), the padded tile
-//           offsets (token_offs_pad) and the tile map;
+//   scan    per expert, exclusive prefix over chunks, then the exclusive
+//           scan over experts (token_offs_raw), the padded tile offsets
+//           (token_offs_pad) and the tile map -- recomputed by every scatter
+//           workgroup from the chunk histograms (integer sums, so all agree);
 //   scatter per chunk, in slot order: a slot's rank among equal experts is
 //           found with wave ballots (no atomics decide a position), so each
 //           expert's slots keep ascending flat order — the stable argsort of
 //           :118 — and every run writes identical bits.
-// For one chunk (M <= 256) the three phases run in a single workgroup launch.
+// Two launches (rows, scan + scatter); for one chunk (M <= 256) the three
+// phases run in a single workgroup launch.
 #include "common.hpp"
 
 namespace fmoe {
@@ -48,29 +50,71 @@ __device__ __forceinline__ int load_id(const AlignParams& p, int64_t f) {
   return v;
 }
 
-// ---- phase 1: per-token sort + chunk histogram
-__device__ void phase_rows(const AlignParams& p, int c, int* h) {
+// A chunk holds at most 256 tokens x 32 slots.
+constexpr int kChunkSlots = kAlignThreads * 32;
+
+// Workgroup barrier that orders LDS only.  Around it the chunked phases store
+// to global addresses that no other thread of the launch reads, so those
+// stores need not drain at every barrier (__syncthreads waits for them).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Copy n consecutive 4-byte values src[0..n) into LDS dst[0..n) (coalesced,
+// 8 loads per thread in flight).  load(i) returns the value of slot i.
+template <typename T, typename Load>
+__device__ __forceinline__ void stage_chunk(T* dst, int n, Load load) {
+  const int tid = threadIdx.x;
+  for (int i0 = 0; i0 < n; i0 += 8 * kAlignThreads) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kAlignThreads + tid;
+      v[u] = i < n ? load(i) : T(0);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kAlignThreads + tid;
+      if (i < n) dst[i] = v[u];
+    }
+  }
+}
+
+// Number of slots in chunk c (256 tokens, the last one partial).
+__device__ __forceinline__ int chunk_slots(const AlignParams& p, int c) {
+  const int64_t f0 = static_cast<int64_t>(c) * kAlignThreads * p.k;
+  const int64_t left = p.M * p.k - f0;
+  return static_cast<int>(left < kAlignThreads * p.k ? left : kAlignThreads * p.k);
+}
+
+// ---- phase 1: per-token sort + chunk histogram.  The chunk's ids and
+// weights are staged in LDS first, so each token's k x k rank comparisons
+// read LDS instead of issuing one dependent global load each.
+__device__ void phase_rows(const AlignParams& p, int c, int* h, int* s_id, float* s_w) {
   const int tid = threadIdx.x;
   for (int e = tid; e < p.E; e += kAlignThreads) h[e] = 0;
-  __syncthreads();
+  const int64_t f0 = static_cast<int64_t>(c) * kAlignThreads * p.k;
+  const int n = chunk_slots(p, c);
+  stage_chunk(s_id, n, [&](int i) { return load_id(p, f0 + i); });
+  stage_chunk(s_w, n, [&](int i) { return p.w[f0 + i]; });
+  lds_barrier();
   const int64_t t = static_cast<int64_t>(c) * kAlignThreads + tid;
   if (t < p.M) {
-    const float* wr = p.w + t * p.k;
+    const int* row = s_id + tid * p.k;
+    const float* wr = s_w + tid * p.k;
     for (int j = 0; j < p.k; ++j) {
-      int idj = load_id(p, t * p.k + j);
+      const int idj = row[j];
       int rank = 0;
       for (int i = 0; i < p.k; ++i) {
-        int idi = load_id(p, t * p.k + i);
+        const int idi = row[i];
         rank += (idi < idj) || (idi == idj && i < j);
       }
-      int64_t f = t * p.k + rank;
+      const int64_t f = t * p.k + rank;
       p.o.expt_indx[f] = idj;
       p.o.expt_scal[f] = wr[j];
       p.sort_col[f] = j;
       if (idj >= 0 && idj < p.E) atomicAdd(&h[idj], 1);
     }
   }
-  __syncthreads();
+  lds_barrier();
   for (int e = tid; e < p.E; e += kAlignThreads) p.chunk_hist[static_cast<int64_t>(c) * p.E + e] = h[e];
 }
 
@@ -84,25 +128,26 @@ __device__ int block_exclusive_scan(int v, int* lds_tmp, int* total) {
     if (lane >= o) x += y;
   }
   if (lane == kWave - 1) lds_tmp[wid] = x;
-  __syncthreads();
+  lds_barrier();
   int wbase = 0, tot = 0;
   for (int i = 0; i < kAlignThreads / kWave; ++i) {
     int s = lds_tmp[i];
     if (i < wid) wbase += s;
     tot += s;
   }
-  __syncthreads();
+  lds_barrier();
   *total = tot;
   return wbase + x - v;
 }
 
 // Tile map (ExptData.block_pid_map) and SGLang expert_ids from the padded
 // tile offsets in LDS: tile tt belongs to the last expert whose offset <= tt.
-__device__ void write_tile_map(const AlignParams& p, const int* offs_pad_lds, int ttot) {
-  const int tid = threadIdx.x;
+// Entries tt = first, first + stride, ... are written by this workgroup.
+__device__ void write_tile_map(const AlignParams& p, const int* offs_pad_lds, int ttot,
+                               int64_t first = -1, int64_t stride = kAlignThreads) {
   const int64_t nblk_cap = p.o.expert_ids ? p.sorted_cap / p.bm + 1 : 0;
   const int64_t lim = p.max_tiles > nblk_cap ? p.max_tiles : nblk_cap;
-  for (int64_t tt = tid; tt < lim; tt += kAlignThreads) {
+  for (int64_t tt = first < 0 ? threadIdx.x : first; tt < lim; tt += stride) {
     int val = -1, ex = -1;
     if (tt < ttot) {
       int lo = 0, hi = p.E;  // offs_pad_lds[lo] <= tt < offs_pad_lds[hi]
@@ -192,26 +237,115 @@ __device__ void phase_scan(const AlignParams& p, const int32_t* hist_in, int* of
   write_tile_map(p, offs_pad_lds, ttot);
 }
 
-// ---- phase 3: stable scatter of one chunk
+// ---- phase 2b (chunked path, inside the scatter launch): every scatter
+// workgroup recomputes the scan from the chunk histograms (C x E integers,
+// read in batches), so no separate one-workgroup scan launch sits between
+// rows and scatter.  Integer sums: every workgroup gets the same offsets,
+// identical to phase_scan's.  Workgroup c keeps in LDS, per expert, its
+// chunk's first slot position (base) and the padded-order shift (padshift);
+// workgroup 0 writes ExptData / histogram outputs, and all workgroups share
+// the tile map.
+__device__ void phase_scan_local(const AlignParams& p, int c, int* base, int* padshift,
+                                 int* offs_pad_lds, int* tmp) {
+  const int tid = threadIdx.x;
+  constexpr int PER = kMaxExperts / kAlignThreads;
+  int hv[PER], bv[PER], tv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) hv[i] = bv[i] = 0;
+  constexpr int kBatch = 8;
+  const int32_t* __restrict__ ch = p.chunk_hist;
+  for (int c0 = 0; c0 < p.n_chunks; c0 += kBatch) {
+    int v[kBatch][PER];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int e = tid * PER + i;
+        v[b][i] = (c0 + b < p.n_chunks && e < p.E) ? ch[static_cast<int64_t>(c0 + b) * p.E + e] : 0;
+      }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if (c0 + b == c) bv[i] = hv[i];
+        hv[i] += v[b][i];
+      }
+  }
+  int hsum = 0, tsum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    tv[i] = (hv[i] + p.bm - 1) / p.bm;
+    hsum += hv[i];
+    tsum += tv[i];
+  }
+  int htot, ttot;
+  int hbase = block_exclusive_scan(hsum, tmp, &htot);
+  int tbase = block_exclusive_scan(tsum, tmp, &ttot);
+  const bool lead = c == 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = tid * PER + i;
+    if (e < p.E) {
+      if (lead) {
+        if (p.o.hist) p.o.hist[e] = hv[i];
+        p.o.offs_raw[e] = hbase;
+        p.o.offs_pad[e] = tbase;
+      }
+      offs_pad_lds[e] = tbase;
+      base[e] = hbase + bv[i];
+      padshift[e] = tbase * p.bm - hbase;
+    }
+    hbase += hv[i];
+    tbase += tv[i];
+  }
+  if (tid == 0) {
+    offs_pad_lds[p.E] = ttot;
+    if (lead) {
+      p.o.offs_raw[p.E] = htot;
+      p.o.offs_pad[p.E] = ttot;
+      p.o.n_tiles[0] = ttot;
+      if (p.o.num_tokens_post_padded) p.o.num_tokens_post_padded[0] = ttot * p.bm;
+    }
+  }
+  lds_barrier();
+  write_tile_map(p, offs_pad_lds, ttot, static_cast<int64_t>(c) * kAlignThreads + tid,
+                 static_cast<int64_t>(p.n_chunks) * kAlignThreads);
+}
+
+// base / padshift of chunk c from the scan outputs in global memory (one
+// workgroup that ran phase_scan itself).
+__device__ void scatter_bases_from_global(const AlignParams& p, int c, int* base, int* padshift) {
+  for (int e = threadIdx.x; e < p.E; e += kAlignThreads) {
+    const int ob = p.o.offs_raw[e];
+    base[e] = ob + p.chunk_base[static_cast<int64_t>(c) * p.E + e];
+    padshift[e] = p.o.offs_pad[e] * p.bm - ob;
+  }
+}
+
+// ---- phase 3: stable scatter of one chunk (base / padshift already in LDS).
+// The chunk's row-sorted ids, weights and source columns are staged in LDS
+// first (all loads in flight), so the k ballot rounds touch no global loads.
 __device__ void phase_scatter(const AlignParams& p, int c, int* run, int (*wcnt)[kMaxExperts],
-                              int* base, int* padshift) {
+                              const int* base, const int* padshift, int* s_e, float* s_scal,
+                              int* s_col) {
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
   for (int e = tid; e < p.E; e += kAlignThreads) {
     run[e] = 0;
     for (int w = 0; w < kAlignThreads / kWave; ++w) wcnt[w][e] = 0;
-    int ob = p.o.offs_raw[e];
-    base[e] = ob + p.chunk_base[static_cast<int64_t>(c) * p.E + e];
-    padshift[e] = p.o.offs_pad[e] * p.bm - ob;
   }
-  __syncthreads();
-  const int64_t n = p.M * p.k;
   const int64_t f0 = static_cast<int64_t>(c) * kAlignThreads * p.k;
+  const int n = chunk_slots(p, c);
+  stage_chunk(s_e, n, [&](int i) { return p.o.expt_indx[f0 + i]; });
+  stage_chunk(s_scal, n, [&](int i) { return p.o.expt_scal[f0 + i]; });
+  if (p.o.sorted_token_ids) stage_chunk(s_col, n, [&](int i) { return p.sort_col[f0 + i]; });
+  lds_barrier();
   const uint64_t lt = (1ull << lane) - 1ull;
   for (int it = 0; it < p.k; ++it) {
-    const int64_t f = f0 + static_cast<int64_t>(it) * kAlignThreads + tid;
+    const int i = it * kAlignThreads + tid;
+    const int64_t f = f0 + i;
     int e = p.E;  // marker: no expert (past the end, or an out-of-range id)
-    if (f < n) {
-      int v = p.o.expt_indx[f];
+    if (i < n) {
+      int v = s_e[i];
       if (v >= 0 && v < p.E) e = v;
       else p.o.gate_indx[f] = -1;
     }
@@ -228,25 +362,25 @@ __device__ void phase_scatter(const AlignParams& p, int c, int* run, int (*wcnt)
     const bool live = e < p.E;
     const bool leader = live && r == cnt - 1;
     if (leader) wcnt[wid][e] = cnt;
-    __syncthreads();
+    lds_barrier();
     if (live) {
       int before = run[e];
       for (int w = 0; w < wid; ++w) before += wcnt[w][e];
       const int pos = base[e] + before + r;
       p.o.topk_indx[pos] = static_cast<int32_t>(f);
       p.o.gate_indx[f] = pos;
-      p.o.gate_scal[pos] = p.o.expt_scal[f];
+      p.o.gate_scal[pos] = s_scal[i];
       if (p.o.sorted_token_ids) {
         const int64_t t = f / p.k;
-        p.o.sorted_token_ids[pos + padshift[e]] = static_cast<int32_t>(t * p.k + p.sort_col[f]);
+        p.o.sorted_token_ids[pos + padshift[e]] = static_cast<int32_t>(t * p.k + s_col[i]);
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (leader) {
       atomicAdd(&run[e], cnt);  // integer sum: order-independent
       wcnt[wid][e] = 0;
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -258,7 +392,9 @@ __device__ void fill_sentinel(const AlignParams& p, int64_t start, int64_t strid
 
 __global__ __launch_bounds__(kAlignThreads) void align_rows_kernel(AlignParams p) {
   __shared__ int h[kMaxExperts];
-  phase_rows(p, blockIdx.x, h);
+  __shared__ int s_id[kChunkSlots];
+  __shared__ float s_w[kChunkSlots];
+  phase_rows(p, blockIdx.x, h, s_id, s_w);
   fill_sentinel(p, static_cast<int64_t>(blockIdx.x) * kAlignThreads + threadIdx.x,
                 static_cast<int64_t>(gridDim.x) * kAlignThreads);
 }
@@ -269,12 +405,19 @@ __global__ __launch_bounds__(kAlignThreads) void align_scan_kernel(AlignParams p
   phase_scan(p, hist_in, offs_pad_lds, tmp);
 }
 
+// Scan (recomputed per workgroup) + stable scatter of chunk blockIdx.x.
 __global__ __launch_bounds__(kAlignThreads) void align_scatter_kernel(AlignParams p) {
   __shared__ int run[kMaxExperts];
   __shared__ int wcnt[kAlignThreads / kWave][kMaxExperts];
   __shared__ int base[kMaxExperts];
   __shared__ int padshift[kMaxExperts];
-  phase_scatter(p, blockIdx.x, run, wcnt, base, padshift);
+  __shared__ int offs_pad_lds[kMaxExperts + 1];
+  __shared__ int tmp[kAlignThreads / kWave];
+  __shared__ int s_e[kChunkSlots];
+  __shared__ float s_scal[kChunkSlots];
+  __shared__ int s_col[kChunkSlots];
+  phase_scan_local(p, blockIdx.x, base, padshift, offs_pad_lds, tmp);
+  phase_scatter(p, blockIdx.x, run, wcnt, base, padshift, s_e, s_scal, s_col);
 }
 
 // All three phases in one workgroup (one chunk: M <= 256).
@@ -284,12 +427,16 @@ __global__ __launch_bounds__(kAlignThreads) void align_small_kernel(AlignParams 
   __shared__ int base[kMaxExperts];
   __shared__ int padshift[kMaxExperts + 1];
   __shared__ int tmp[kAlignThreads / kWave];
+  __shared__ int s_a[kChunkSlots];
+  __shared__ float s_b[kChunkSlots];
+  __shared__ int s_c[kChunkSlots];
   fill_sentinel(p, threadIdx.x, kAlignThreads);
-  phase_rows(p, 0, run);
+  phase_rows(p, 0, run, s_a, s_b);
   __syncthreads();
   phase_scan(p, nullptr, padshift, tmp);
   __syncthreads();
-  phase_scatter(p, 0, run, wcnt, base, padshift);
+  scatter_bases_from_global(p, 0, base, padshift);
+  phase_scatter(p, 0, run, wcnt, base, padshift, s_a, s_b, s_c);
 }
 
 
@@ -504,7 +651,6 @@ extern "C" int fmoe_align_ex(const int32_t* topk_ids, const float* topk_weights,
     align_small_kernel<<<1, kAlignThreads, 0, s>>>(p);
   } else {
     align_rows_kernel<<<static_cast<unsigned>(C), kAlignThreads, 0, s>>>(p);
-    align_scan_kernel<<<1, kAlignThreads, 0, s>>>(p, nullptr);
     align_scatter_kernel<<<static_cast<unsigned>(C), kAlignThreads, 0, s>>>(p);
   }
   return check_launch("align");

@@ -320,7 +320,7 @@ def test_bias_swiglu(M, alpha, limit, on_input):
 
 
 # ------------------------------------------------------------ expert parallel
-@pytest.mark.parametrize("M", [3, 200])
+@pytest.mark.parametrize("M", [3, 200, 700])  # 700: several 256-token routing chunks
 def test_expert_map(M):
     """expert_map / global_num_experts (ops/fused_moe.py:145-146,160): identity
     map equals no map bit for bit; a two-rank split matches the oracle per rank
