@@ -33,24 +33,21 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
-// fp32 -> float8_e4m3fn, round to nearest even.  |f| must already be clamped
-// to <= 448 (callers clamp), so no saturation / NaN path is needed.
-// Normals: keep 3 mantissa bits of the fp32 pattern with RNE, rebias the
-// exponent from 127 to 7.  Below 2^-6 (subnormal): the value in units of
-// 2^-9, rounded to nearest even, is the code itself.
-__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t sign = (u >> 24) & 0x80u;
-  float a = fabsf(f);
-  uint32_t code;
-  if (a < 0.015625f) {
-    code = static_cast<uint32_t>(__builtin_rintf(a * 512.0f));
-  } else {
-    uint32_t au = __float_as_uint(a);
-    uint32_t t = (au + 0x7ffffu + ((au >> 20) & 1u)) >> 20;
-    code = t - (120u << 3);
-  }
-  return sign | code;
+// v / s correctly rounded (as a plain division), then clamped to the e4m3
+// range: v * (1/s) plus one FMA-residual correction (inv = 1/s, itself
+// correctly rounded), which restores the rounding the reciprocal product alone
+// can miss.  Cheaper than a division per element.
+__device__ __forceinline__ float fp8_qdiv(float v, float s, float inv) {
+  const float q0 = v * inv;
+  const float r = __builtin_fmaf(-q0, s, v);
+  return fminf(fmaxf(__builtin_fmaf(r, inv, q0), -kFp8Max), kFp8Max);
+}
+
+// Four values in the e4m3 range -> packed OCP e4m3 bytes (hardware RNE
+// conversion; byte i = value i).
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+  const int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true));
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {

@@ -406,20 +406,12 @@ __global__ __launch_bounds__(kThreads * RB, (WT == WType::kInt4 && PIPE == 1 && 
       amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
       const float sa_row = fmaxf(amax, kFp8Eps) / kFp8Max;  // scale of row lane%16
       const float inv = 1.0f / sa_row;
-      // x / sa_row as the quant pass computes it (correctly rounded): one
-      // FMA-residual correction of x * (1/sa_row) restores the rounding that
-      // the reciprocal product alone misses, so the fp8 codes agree.
-      auto qdiv = [&](float v) {
-        const float q0 = v * inv;
-        const float r = __builtin_fmaf(-q0, sa_row, v);
-        return fminf(fmaxf(__builtin_fmaf(r, inv, q0), -kFp8Max), kFp8Max);
-      };
+      // x / sa_row and the e4m3 codes exactly as the quant pass computes them
       int qa[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int w = __builtin_amdgcn_cvt_pk_fp8_f32(qdiv(x[4 * i]), qdiv(x[4 * i + 1]), 0, false);
-        qa[i] = __builtin_amdgcn_cvt_pk_fp8_f32(qdiv(x[4 * i + 2]), qdiv(x[4 * i + 3]), w, true);
-      }
+      for (int i = 0; i < 8; ++i)
+        qa[i] = static_cast<int>(pack_e4m3x4(fp8_qdiv(x[4 * i], sa_row, inv), fp8_qdiv(x[4 * i + 1], sa_row, inv),
+                                             fp8_qdiv(x[4 * i + 2], sa_row, inv), fp8_qdiv(x[4 * i + 3], sa_row, inv)));
       const i32x8_t a = i32x8_t{qa[0], qa[1], qa[2], qa[3], qa[4], qa[5], qa[6], qa[7]};
       // output rows of this lane are 4*(lane/16) + r: fetch their scales
       float sa[4];

@@ -506,16 +506,15 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
         for (int w = 0; w < C::WAVES_N; ++w) amax = fmaxf(amax, amax_lds[r * C::WAVES_N + w]);
         const float sc = fmaxf(amax, kFp8Eps) / kFp8Max;
+        const float inv = 1.0f / sc;
         if (s >= row_end) continue;
         uint8_t* q = p.act_q + static_cast<int64_t>(s) * p.N_act;
 #pragma unroll
         for (int j = 0; j < NI / 2; ++j) {
           const int64_t col = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2) + j * 16 + ocol;
-          uint32_t word = 0;
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            word |= f32_to_e4m3(fminf(fmaxf(v[i][j][c] / sc, -kFp8Max), kFp8Max)) << (8 * c);
-          *reinterpret_cast<uint32_t*>(q + col) = word;
+          *reinterpret_cast<uint32_t*>(q + col) =
+              pack_e4m3x4(fp8_qdiv(v[i][j][0], sc, inv), fp8_qdiv(v[i][j][1], sc, inv),
+                          fp8_qdiv(v[i][j][2], sc, inv), fp8_qdiv(v[i][j][3], sc, inv));
         }
         if (wn == 0 && ((lane >> 2) & 3) == 0) p.act_qs[static_cast<int64_t>(s) * ngrp + nt] = sc;
       }

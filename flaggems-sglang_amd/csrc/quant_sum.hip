@@ -30,13 +30,11 @@ __global__ __launch_bounds__(256) void quant_fp8_group_kernel(const uint16_t* __
 #pragma unroll
   for (int o = TPG / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, kWave));
   const float s = fmaxf(amax, kFp8Eps) / kFp8Max;
-  uint32_t lo = 0, hi = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float t = fminf(fmaxf(f[i] / s, -kFp8Max), kFp8Max);
-    uint32_t c = f32_to_e4m3(t);
-    if (i < 4) lo |= c << (8 * i); else hi |= c << (8 * (i - 4));
-  }
+  const float inv = 1.0f / s;
+  const uint32_t lo = pack_e4m3x4(fp8_qdiv(f[0], s, inv), fp8_qdiv(f[1], s, inv),
+                                  fp8_qdiv(f[2], s, inv), fp8_qdiv(f[3], s, inv));
+  const uint32_t hi = pack_e4m3x4(fp8_qdiv(f[4], s, inv), fp8_qdiv(f[5], s, inv),
+                                  fp8_qdiv(f[6], s, inv), fp8_qdiv(f[7], s, inv));
   if (!live) return;
   *reinterpret_cast<uint2*>(q + vv * 8) = make_uint2(lo, hi);
   if ((threadIdx.x % TPG) == 0) {
