@@ -61,6 +61,7 @@ ALIGN_CASES = [
     (257, 8, 2, 0.0), (1024, 128, 8, 0.5), (8192, 128, 8, 0.5), (4096, 256, 8, 0.0),
     (8192, 256, 8, 0.0), (4096, 8, 2, 0.0), (3000, 1024, 3, 2.0),
     (600, 64, 32, 0.0),  # k = 32: full 8192-slot chunks in the chunked path
+    (40000, 256, 8, 0.0),  # 157 chunks: every scatter workgroup rescans 20 batches
 ]
 
 
