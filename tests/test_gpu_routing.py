@@ -62,6 +62,9 @@ ALIGN_CASES = [
     (8192, 256, 8, 0.0), (4096, 8, 2, 0.0), (3000, 1024, 3, 2.0),
     (600, 64, 32, 0.0),  # k = 32: full 8192-slot chunks in the chunked path
     (40000, 256, 8, 0.0),  # 157 chunks: every scatter workgroup rescans 20 batches
+    # one-workgroup kernel (one chunk, more than 1024 slots) and the chunked
+    # path with a one-token last chunk
+    (129, 32, 8, 0.0), (200, 64, 8, 1.0), (257, 16, 8, 0.0),
 ]
 
 
