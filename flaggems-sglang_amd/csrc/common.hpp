@@ -33,14 +33,17 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
-// v / s correctly rounded (as a plain division), then clamped to the e4m3
-// range: v * (1/s) plus one FMA-residual correction (inv = 1/s, itself
+// v / s correctly rounded (as a plain division, s > 0), then clamped to the
+// e4m3 range: v * (1/s) plus one FMA-residual correction (inv = 1/s, itself
 // correctly rounded), which restores the rounding the reciprocal product alone
-// can miss.  Cheaper than a division per element.
+// can miss.  Cheaper than a division per element.  The correction step turns
+// a -0 quotient into +0 (+0 + -0), so the sign is copied back from v (a
+// division keeps it: -0 / s = -0, and -0 quantizes to the e4m3 byte 0x80).
 __device__ __forceinline__ float fp8_qdiv(float v, float s, float inv) {
   const float q0 = v * inv;
   const float r = __builtin_fmaf(-q0, s, v);
-  return fminf(fmaxf(__builtin_fmaf(r, inv, q0), -kFp8Max), kFp8Max);
+  const float q = __builtin_copysignf(__builtin_fmaf(r, inv, q0), v);
+  return fminf(fmaxf(q, -kFp8Max), kFp8Max);
 }
 
 // Four values in the e4m3 range -> packed OCP e4m3 bytes (hardware RNE

@@ -113,6 +113,51 @@ def test_align_empty_experts_and_all_one_expert():
     assert int(z.n_tiles.item()) == 0 and torch.all(z.offs_raw == 0)
 
 
+def _e4m3_tie_rows():
+    """Rows of 128-element groups whose scale is a power of two (one element
+    is +-448 * 2^j), so x / scale is exact and lands on chosen points: every
+    e4m3 rounding midpoint (normal and subnormal), one bf16 ulp either side of
+    it, and the e4m3 values themselves, with both signs."""
+    mags = []
+    for e in range(-6, 9):                      # normal binades 2^-6 .. 2^8
+        for f in range(8):
+            v = (1 + f / 8) * 2.0 ** e
+            mid = (1 + (2 * f + 1) / 16) * 2.0 ** e
+            if mid <= 448:
+                mags += [v, mid]
+    for i in range(8):                          # subnormal codes and midpoints
+        mags += [i * 2.0 ** -9, (2 * i + 1) * 2.0 ** -10]
+    base = torch.tensor(mags, dtype=torch.float32)
+    ulp = torch.tensor(mags, dtype=torch.bfloat16).float()
+    up = torch.nextafter(ulp.bfloat16(), torch.tensor(float("inf"), dtype=torch.bfloat16)).float()
+    dn = torch.nextafter(ulp.bfloat16(), torch.tensor(0.0, dtype=torch.bfloat16)).float()
+    vals = torch.cat([base, up, dn])
+    vals = torch.cat([vals, -vals])             # includes -0.0 (e4m3 byte 0x80)
+    n_grp = (vals.numel() + 126) // 127
+    rows = []
+    for j in (-12, -3, 0, 5):
+        g = torch.zeros(n_grp, 128)
+        flat = torch.zeros(n_grp * 127)
+        flat[: vals.numel()] = vals
+        g[:, 1:] = flat.view(n_grp, 127)
+        g[:, 0] = 448.0 * (-1) ** torch.arange(n_grp)   # the group amax: +-448
+        rows.append(g * 2.0 ** j)
+    x = torch.cat(rows).view(-1, 256 if n_grp % 2 == 0 else 128)
+    return x.to(torch.bfloat16)
+
+
+def test_quant_fp8_ties_and_subnormals():
+    """Exact rounding midpoints and e4m3 subnormals: the GPU's division and
+    RNE conversion give the oracle's bytes (round half to even)."""
+    x = _e4m3_tie_rows()
+    assert torch.equal(x.float(), x.float().bfloat16().float())
+    q_ref, s_ref = O.per_token_group_quant_fp8(x)
+    assert torch.all((s_ref.log2() == s_ref.log2().round()))  # power-of-two scales
+    q, s = flaggems_sglang.per_token_group_quant_fp8(x.to(DEV))
+    assert torch.equal(s.cpu(), s_ref)
+    assert torch.equal(q.cpu().view(torch.uint8), q_ref.view(torch.uint8))
+
+
 @pytest.mark.parametrize("M,K", [(1, 128), (7, 7168), (256, 2048), (4096, 7168)])
 def test_quant_fp8_bit_exact(M, K):
     g = torch.Generator().manual_seed(M + K)
