@@ -92,6 +92,18 @@ def test_fused_moe_input_gate(shape):
     _close(res, ref, 2e-2)
 
 
+@pytest.mark.parametrize("topk", [1, 6, 12])
+@pytest.mark.parametrize("M", [3, 300])
+def test_topk_counts(M, topk):
+    """Top-k counts outside the BASELINE set: 1 (switch routing), 6 and 12
+    (the top-k sum's 8-term batches end part-full), decode and prefill."""
+    K, N, E = 256, 384, 32
+    x, w1, w2, tw, ti = _ref_inputs(M, K, N, E, topk)
+    w13, w2t = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
+    out = flaggems_sglang.fused_experts(x.to(DEV), w13.to(DEV), w2t.to(DEV), tw.to(DEV), ti.to(DEV))
+    _close(out, O.fused_experts(x, w13, w2t, tw, ti), 2e-2)
+
+
 @pytest.mark.parametrize("path", [1, 2])
 @pytest.mark.parametrize("M", [1, 16, 64, 300])
 def test_fused_experts_both_paths(M, path):
