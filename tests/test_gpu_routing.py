@@ -128,9 +128,9 @@ def _e4m3_tie_rows():
     for i in range(8):                          # subnormal codes and midpoints
         mags += [i * 2.0 ** -9, (2 * i + 1) * 2.0 ** -10]
     base = torch.tensor(mags, dtype=torch.float32)
-    ulp = torch.tensor(mags, dtype=torch.bfloat16).float()
-    up = torch.nextafter(ulp.bfloat16(), torch.tensor(float("inf"), dtype=torch.bfloat16)).float()
-    dn = torch.nextafter(ulp.bfloat16(), torch.tensor(0.0, dtype=torch.bfloat16)).float()
+    b16 = base.bfloat16()                       # exact: every point has <= 4 significant bits
+    up = torch.nextafter(b16, torch.tensor(float("inf"), dtype=torch.bfloat16)).float()
+    dn = torch.nextafter(b16, torch.tensor(0.0, dtype=torch.bfloat16)).float()
     vals = torch.cat([base, up, dn])
     vals = torch.cat([vals, -vals])             # includes -0.0 (e4m3 byte 0x80)
     n_grp = (vals.numel() + 126) // 127
