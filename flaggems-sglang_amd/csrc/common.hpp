@@ -37,12 +37,14 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to
 // e4m3 range: v * (1/s) plus one FMA-residual correction (inv = 1/s, itself
 // correctly rounded), which restores the rounding the reciprocal product alone
 // can miss.  Cheaper than a division per element.  The correction step turns
-// a -0 quotient into +0 (+0 + -0), so the sign is copied back from v (a
-// division keeps it: -0 / s = -0, and -0 quantizes to the e4m3 byte 0x80).
+// a -0 quotient into +0 (+0 + -0), so the sign is copied back from q0, which
+// has v's sign like the division (-0 / s = -0, the e4m3 byte 0x80); taking
+// it from q0 rather than v keeps v's live range (and the kernels' register
+// counts) as without the fix.
 __device__ __forceinline__ float fp8_qdiv(float v, float s, float inv) {
   const float q0 = v * inv;
   const float r = __builtin_fmaf(-q0, s, v);
-  const float q = __builtin_copysignf(__builtin_fmaf(r, inv, q0), v);
+  const float q = __builtin_copysignf(__builtin_fmaf(r, inv, q0), q0);
   return fminf(fmaxf(q, -kFp8Max), kFp8Max);
 }
 
