@@ -8,6 +8,7 @@ namespace fmoe {
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s);
 int decode_int4_row_split(int64_t max_tiles);
 int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
+int launch_gemm2_sum_token(const GemmParams& q, int E, int k, float scale, void* out, hipStream_t s);
 int dequant_4bit(int wtype, const void* q, const void* scale, const void* zeros, int64_t E,
                  int64_t R, int64_t K, uint16_t* out, hipStream_t s);
 int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t M, int k, int64_t K,
@@ -505,6 +506,12 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
                           a->routed_scaling_factor, a->out, s);
   }
   if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm1Silu, g1, s)) return st;
+#ifndef FMOE_TOKEN_SUM
+#define FMOE_TOKEN_SUM 1
+#endif
+  // one bf16 token: GEMM2 and the top-k sum in one launch
+  if (FMOE_TOKEN_SUM && a->M == 1 && a->wtype == FMOE_W_BF16 && a->top_k <= 32)
+    return launch_gemm2_sum_token(g2, a->E, a->top_k, a->routed_scaling_factor, a->out, s);
   if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm2, g2, s)) return st;
   return moe_sum_flat(y, L.splits, a->topk_ids, a->E, a->M, a->top_k, a->K, a->routed_scaling_factor,
                       a->out, s);

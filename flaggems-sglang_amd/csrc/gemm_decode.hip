@@ -1296,4 +1296,85 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   return fmoe_host::check_launch("gemm_decode");
 }
 
+// ---- single-token bf16 decode: GEMM2 and the top-k sum in one launch.
+// out[r] = bf16(scale * sum_j g_j * (w2[e_j][r] . act_j + b2[e_j][r])), the
+// slots j in ascending order (dropped ids skipped), as fmoe_moe_sum adds the
+// per-slot rows of the two-launch path.  A workgroup owns one output row, so
+// the grid (K rows) spreads evenly over the CUs; its 16 groups of 16 lanes
+// take the (slot j, reduction slice s) items, S = ceil(16 / k) slices so
+// that small k still fills the groups; each lane dots 8 columns per 16-byte
+// load, 4 loads in flight; a group reduces with xor shuffles and the item
+// sums meet in LDS, added in fixed (j, s) order: every run gives the same bits.
+namespace decode {
+__global__ __launch_bounds__(256) void gemm2_sum_token_kernel(GemmParams q, int E, int k, float scale,
+                                                              uint16_t* __restrict__ out) {
+  constexpr int kGroups = 256 / 16;
+  __shared__ float part[32 * kGroups];  // [j * S + s]: k * S <= 32 * 16
+  const int grp = threadIdx.x / 16, sub = threadIdx.x % 16;
+  const int64_t K = q.Nout, N = q.Kred;
+  const int64_t row = blockIdx.x;
+  const int S = k >= kGroups ? 1 : (kGroups + k - 1) / k;
+  const int64_t slice = ((N / 8 + S - 1) / S) * 8;
+  const uint16_t* __restrict__ w2 = reinterpret_cast<const uint16_t*>(q.B);
+  const uint16_t* __restrict__ act = reinterpret_cast<const uint16_t*>(q.A);
+  for (int it = grp; it < k * S; it += kGroups) {
+    const int j = it / S, sl = it - (it / S) * S;
+    const int e = q.tiny_ids[j];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (e >= 0 && e < E) {
+      const uint16_t* wr = w2 + (static_cast<int64_t>(e) * K + row) * N;
+      const uint16_t* ar = act + static_cast<int64_t>(j) * N;
+      const int64_t n1 = min(N, (sl + 1) * slice);
+      for (int64_t n = sl * slice + sub * 8; n < n1; n += 4 * 128) {
+        i32x4_t w[4], a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int64_t c = n + u * 128 < n1 ? n + u * 128 : n;  // past the end: reread, not added
+          w[u] = *reinterpret_cast<const i32x4_t*>(wr + c);
+          a[u] = *reinterpret_cast<const i32x4_t*>(ar + c);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (n + u * 128 >= n1) continue;
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const uint32_t wv = static_cast<uint32_t>(w[u][h]), av = static_cast<uint32_t>(a[u][h]);
+            acc[u] = __builtin_fmaf(__uint_as_float(wv << 16), __uint_as_float(av << 16), acc[u]);
+            acc[u] = __builtin_fmaf(__uint_as_float(wv & 0xffff0000u), __uint_as_float(av & 0xffff0000u), acc[u]);
+          }
+        }
+      }
+    }
+    float v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    if (sub == 0) part[it] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float y = 0.f;
+    for (int j = 0; j < k; ++j) {
+      const int e = q.tiny_ids[j];
+      if (e < 0 || e >= E) continue;
+      float d = 0.f;
+      for (int sl = 0; sl < S; ++sl) d += part[j * S + sl];
+      if (q.bias) d += q.bias[static_cast<int64_t>(e) * K + row];
+      y += d * (q.gamma ? q.tiny_w[j] : 1.0f);
+    }
+    out[row] = f32_to_bf16(y * scale);
+  }
+}
+}  // namespace decode
+
+// Single-token bf16 GEMM2 + top-k sum (q as for the two-launch path: A = the
+// GEMM1 rows of the token's k slots, B = w2, tiny_ids / tiny_w the routing).
+int launch_gemm2_sum_token(const GemmParams& q, int E, int k, float scale, void* out, hipStream_t s) {
+  if (k < 1 || k > 32 || q.Kred % 8 != 0 || q.Nout < 1)
+    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: k <= 32, N %% 8 == 0");
+  if (q.Nout > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: K too large");
+  decode::gemm2_sum_token_kernel<<<dim3(static_cast<unsigned>(q.Nout)), dim3(256), 0, s>>>(
+      q, E, k, scale, static_cast<uint16_t*>(out));
+  return fmoe_host::check_launch("gemm2_sum_token");
+}
+
 }  // namespace fmoe
