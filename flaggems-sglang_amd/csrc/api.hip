@@ -509,8 +509,11 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
 #ifndef FMOE_TOKEN_SUM
 #define FMOE_TOKEN_SUM 1
 #endif
-  // one bf16 token: GEMM2 and the top-k sum in one launch
-  if (FMOE_TOKEN_SUM && a->M == 1 && a->wtype == FMOE_W_BF16 && a->top_k <= 32)
+#ifndef FMOE_TOKEN_SUM_MAX_M
+#define FMOE_TOKEN_SUM_MAX_M 1
+#endif
+  // small bf16 batches: GEMM2 and the top-k sum in one launch
+  if (FMOE_TOKEN_SUM && a->M <= FMOE_TOKEN_SUM_MAX_M && a->wtype == FMOE_W_BF16 && a->M * a->top_k <= 32)
     return launch_gemm2_sum_token(g2, a->E, a->top_k, a->routed_scaling_factor, a->out, s);
   if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm2, g2, s)) return st;
   return moe_sum_flat(y, L.splits, a->topk_ids, a->E, a->M, a->top_k, a->K, a->routed_scaling_factor,

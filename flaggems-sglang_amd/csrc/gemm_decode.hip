@@ -1296,34 +1296,37 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   return fmoe_host::check_launch("gemm_decode");
 }
 
-// ---- single-token bf16 decode: GEMM2 and the top-k sum in one launch.
-// out[r] = bf16(scale * sum_j g_j * (w2[e_j][r] . act_j + b2[e_j][r])), the
-// slots j in ascending order (dropped ids skipped), as fmoe_moe_sum adds the
-// per-slot rows of the two-launch path.  A workgroup owns one output row, so
-// the grid (K rows) spreads evenly over the CUs; its 16 groups of 16 lanes
-// take the (slot j, reduction slice s) items, S = ceil(16 / k) slices so
-// that small k still fills the groups; each lane dots 8 columns per 16-byte
-// load, 4 loads in flight; a group reduces with xor shuffles and the item
-// sums meet in LDS, added in fixed (j, s) order: every run gives the same bits.
+// ---- small bf16 decode batches (M * k <= 32 slots): GEMM2 and the top-k sum
+// in one launch.  out[t][r] = bf16(scale * sum_j g_tj * (w2[e_tj][r] . act_tj
+// + b2[e_tj][r])), each token's slots j in ascending order (dropped ids
+// skipped), as fmoe_moe_sum adds the per-slot rows of the two-launch path.  A
+// workgroup owns one output row, so the grid (K rows) spreads evenly over the
+// CUs; its 16 groups of 16 lanes take the (slot, reduction slice) items, S =
+// ceil(16 / slots) slices so that few slots still fill the groups; each lane
+// dots 8 columns per 16-byte load, 4 loads in flight; a group reduces with
+// xor shuffles and the item sums meet in LDS, added in fixed (slot, slice)
+// order: every run gives the same bits.
 namespace decode {
+constexpr int kTokSlots = 32;
 __global__ __launch_bounds__(256) void gemm2_sum_token_kernel(GemmParams q, int E, int k, float scale,
                                                               uint16_t* __restrict__ out) {
   constexpr int kGroups = 256 / 16;
-  __shared__ float part[32 * kGroups];  // [j * S + s]: k * S <= 32 * 16
+  __shared__ float part[kTokSlots];  // [slot * S + s]: slots * S <= 32
   const int grp = threadIdx.x / 16, sub = threadIdx.x % 16;
   const int64_t K = q.Nout, N = q.Kred;
   const int64_t row = blockIdx.x;
-  const int S = k >= kGroups ? 1 : (kGroups + k - 1) / k;
+  const int slots = static_cast<int>(q.n_tokens) * k;
+  const int S = slots >= kGroups ? 1 : (kGroups + slots - 1) / slots;
   const int64_t slice = ((N / 8 + S - 1) / S) * 8;
   const uint16_t* __restrict__ w2 = reinterpret_cast<const uint16_t*>(q.B);
   const uint16_t* __restrict__ act = reinterpret_cast<const uint16_t*>(q.A);
-  for (int it = grp; it < k * S; it += kGroups) {
-    const int j = it / S, sl = it - (it / S) * S;
-    const int e = q.tiny_ids[j];
+  for (int it = grp; it < slots * S; it += kGroups) {
+    const int f = it / S, sl = it - (it / S) * S;  // flat slot t * k + j, slice
+    const int e = q.tiny_ids[f];
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     if (e >= 0 && e < E) {
       const uint16_t* wr = w2 + (static_cast<int64_t>(e) * K + row) * N;
-      const uint16_t* ar = act + static_cast<int64_t>(j) * N;
+      const uint16_t* ar = act + static_cast<int64_t>(f) * N;
       const int64_t n1 = min(N, (sl + 1) * slice);
       for (int64_t n = sl * slice + sub * 8; n < n1; n += 4 * 128) {
         i32x4_t w[4], a[4];
@@ -1351,26 +1354,30 @@ __global__ __launch_bounds__(256) void gemm2_sum_token_kernel(GemmParams q, int 
     if (sub == 0) part[it] = v;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  const int t = threadIdx.x;
+  if (t < q.n_tokens) {
     float y = 0.f;
     for (int j = 0; j < k; ++j) {
-      const int e = q.tiny_ids[j];
+      const int f = t * k + j;
+      const int e = q.tiny_ids[f];
       if (e < 0 || e >= E) continue;
       float d = 0.f;
-      for (int sl = 0; sl < S; ++sl) d += part[j * S + sl];
+      for (int sl = 0; sl < S; ++sl) d += part[f * S + sl];
       if (q.bias) d += q.bias[static_cast<int64_t>(e) * K + row];
-      y += d * (q.gamma ? q.tiny_w[j] : 1.0f);
+      y += d * (q.gamma ? q.tiny_w[f] : 1.0f);
     }
-    out[row] = f32_to_bf16(y * scale);
+    out[static_cast<int64_t>(t) * K + row] = f32_to_bf16(y * scale);
   }
 }
 }  // namespace decode
 
-// Single-token bf16 GEMM2 + top-k sum (q as for the two-launch path: A = the
-// GEMM1 rows of the token's k slots, B = w2, tiny_ids / tiny_w the routing).
+// Small-batch bf16 GEMM2 + top-k sum (q as for the two-launch path: A = the
+// GEMM1 rows of the batch's flat slots, B = w2, tiny_ids / tiny_w / n_tokens
+// the routing).
 int launch_gemm2_sum_token(const GemmParams& q, int E, int k, float scale, void* out, hipStream_t s) {
-  if (k < 1 || k > 32 || q.Kred % 8 != 0 || q.Nout < 1)
-    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: k <= 32, N %% 8 == 0");
+  if (k < 1 || q.n_tokens < 1 || q.n_tokens * k > decode::kTokSlots || q.Kred % 8 != 0 || q.Nout < 1)
+    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: M * k <= %d, N %% 8 == 0",
+                           decode::kTokSlots);
   if (q.Nout > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: K too large");
   decode::gemm2_sum_token_kernel<<<dim3(static_cast<unsigned>(q.Nout)), dim3(256), 0, s>>>(
       q, E, k, scale, static_cast<uint16_t*>(out));
