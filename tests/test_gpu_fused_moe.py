@@ -93,15 +93,18 @@ def test_fused_moe_input_gate(shape):
 
 
 @pytest.mark.parametrize("topk", [1, 6, 12])
-@pytest.mark.parametrize("M", [3, 300])
+@pytest.mark.parametrize("M", [1, 3, 300])
 def test_topk_counts(M, topk):
     """Top-k counts outside the BASELINE set: 1 (switch routing), 6 and 12
-    (the top-k sum's 8-term batches end part-full), decode and prefill."""
+    (the top-k sum's 8-term batches end part-full), one token (GEMM2 and the
+    top-k sum in one launch), decode and prefill; bit-identical reruns."""
     K, N, E = 256, 384, 32
     x, w1, w2, tw, ti = _ref_inputs(M, K, N, E, topk)
     w13, w2t = w1.transpose(1, 2).contiguous(), w2.transpose(1, 2).contiguous()
-    out = flaggems_sglang.fused_experts(x.to(DEV), w13.to(DEV), w2t.to(DEV), tw.to(DEV), ti.to(DEV))
+    args = (x.to(DEV), w13.to(DEV), w2t.to(DEV), tw.to(DEV), ti.to(DEV))
+    out = flaggems_sglang.fused_experts(*args)
     _close(out, O.fused_experts(x, w13, w2t, tw, ti), 2e-2)
+    assert torch.equal(out, flaggems_sglang.fused_experts(*args))
 
 
 @pytest.mark.parametrize("path", [1, 2])
