@@ -8,6 +8,7 @@ namespace fmoe {
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s);
 int decode_int4_row_split(int64_t max_tiles);
 int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
+int launch_gemm1_token(const GemmParams& p, int E, int k, hipStream_t s);
 int launch_gemm2_sum_token(const GemmParams& q, int E, int k, float scale, void* out, hipStream_t s);
 int dequant_4bit(int wtype, const void* q, const void* scale, const void* zeros, int64_t E,
                  int64_t R, int64_t K, uint16_t* out, hipStream_t s);
@@ -505,7 +506,15 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
     return moe_sum_planes(y, L.splits, nullptr, a->topk_ids, a->E, a->M, a->top_k, a->K,
                           a->routed_scaling_factor, a->out, s);
   }
-  if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm1Silu, g1, s)) return st;
+#ifndef FMOE_TOKEN_G1
+#define FMOE_TOKEN_G1 1
+#endif
+  // one bf16 token: GEMM1 as a row-parallel dot (more workgroups than 64-row blocks)
+  if (FMOE_TOKEN_G1 && a->M == 1 && a->wtype == FMOE_W_BF16) {
+    if (int st = launch_gemm1_token(g1, a->E, a->top_k, s)) return st;
+  } else if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm1Silu, g1, s)) {
+    return st;
+  }
 #ifndef FMOE_TOKEN_SUM
 #define FMOE_TOKEN_SUM 1
 #endif

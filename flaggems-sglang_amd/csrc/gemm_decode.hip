@@ -1371,6 +1371,79 @@ __global__ __launch_bounds__(256) void gemm2_sum_token_kernel(GemmParams q, int 
 }
 }  // namespace decode
 
+// ---- single-token bf16 decode GEMM1: act[j][c] = act(w13[e_j] rows of column
+// c . x), one workgroup per (slot j, 8 columns): its 16 groups of 16 lanes
+// each dot one weight row (the gate or up row of a column) with the token's
+// x, 16-byte loads, 4 in flight; the epilogue is the row-block kernel's
+// (gemm1_bias / gemm1_act, bf16 activation row).  Small N_act has more
+// workgroups here than 64-row blocks give (Qwen3: 768 instead of 192).
+namespace decode {
+constexpr int kTokCols = 8;
+template <int ACT>
+__global__ __launch_bounds__(256) void gemm1_token_kernel(GemmParams p, int E) {
+  __shared__ float dots[2 * kTokCols];
+  const int grp = threadIdx.x / 16, sub = threadIdx.x % 16;
+  const int64_t nblk = (p.N_act + kTokCols - 1) / kTokCols;
+  const int j = static_cast<int>(blockIdx.x / nblk);
+  const int64_t c0 = (blockIdx.x - static_cast<int64_t>(j) * nblk) * kTokCols;
+  const int e = p.tiny_ids[j];
+  if (e < 0 || e >= E) return;  // dropped slot: GEMM2 skips it
+  const int64_t K = p.Kred;
+  const int64_t col = c0 + grp / 2;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (col < p.N_act) {
+    const uint16_t* wr = reinterpret_cast<const uint16_t*>(p.B) +
+                         (static_cast<int64_t>(e) * p.Nout + gemm1_row(ACT, p.N_act, col, grp % 2)) * K;
+    const uint16_t* xr = reinterpret_cast<const uint16_t*>(p.A);
+    for (int64_t n = sub * 8; n < K; n += 4 * 128) {
+      i32x4_t w[4], a[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t c = n + u * 128 < K ? n + u * 128 : n;  // past the end: reread, not added
+        w[u] = *reinterpret_cast<const i32x4_t*>(wr + c);
+        a[u] = *reinterpret_cast<const i32x4_t*>(xr + c);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (n + u * 128 >= K) continue;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const uint32_t wv = static_cast<uint32_t>(w[u][h]), av = static_cast<uint32_t>(a[u][h]);
+          acc[u] = __builtin_fmaf(__uint_as_float(wv << 16), __uint_as_float(av << 16), acc[u]);
+          acc[u] = __builtin_fmaf(__uint_as_float(wv & 0xffff0000u), __uint_as_float(av & 0xffff0000u), acc[u]);
+        }
+      }
+    }
+  }
+  float v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  if (sub == 0) dots[grp] = v;
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < kTokCols && c0 + t < p.N_act) {
+    const float g = p.gamma ? p.tiny_w[j] : 1.0f;
+    float gb, ub;
+    gemm1_bias<ACT>(p, e, c0 + t, gb, ub);
+    uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(j) * p.N_act;
+    act[c0 + t] = f32_to_bf16(gemm1_act<ACT>(p, dots[2 * t], dots[2 * t + 1], gb, ub, g));
+  }
+}
+}  // namespace decode
+
+// Single-token bf16 GEMM1 (p as for the row-block kernel with tiny routing).
+int launch_gemm1_token(const GemmParams& p, int E, int k, hipStream_t s) {
+  if (p.n_tokens != 1 || k < 1 || p.Kred % 8 != 0)
+    return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm1_token: one token, K %% 8 == 0");
+  const int64_t grid = static_cast<int64_t>(k) * ((p.N_act + decode::kTokCols - 1) / decode::kTokCols);
+  if (grid > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm1_token: grid too large");
+  const dim3 g(static_cast<unsigned>(grid)), b(256);
+  if (p.act == kActSwiglu) decode::gemm1_token_kernel<kActSwiglu><<<g, b, 0, s>>>(p, E);
+  else if (p.act == kActGelu) decode::gemm1_token_kernel<kActGelu><<<g, b, 0, s>>>(p, E);
+  else decode::gemm1_token_kernel<kActSilu><<<g, b, 0, s>>>(p, E);
+  return fmoe_host::check_launch("gemm1_token");
+}
+
 // Small-batch bf16 GEMM2 + top-k sum (q as for the two-launch path: A = the
 // GEMM1 rows of the batch's flat slots, B = w2, tiny_ids / tiny_w / n_tokens
 // the routing).
