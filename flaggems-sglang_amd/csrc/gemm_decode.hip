@@ -1308,23 +1308,26 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
 // order: every run gives the same bits.
 namespace decode {
 constexpr int kTokSlots = 32;
+template <int ROWS>
 __global__ __launch_bounds__(256) void gemm2_sum_token_kernel(GemmParams q, int E, int k, float scale,
                                                               uint16_t* __restrict__ out) {
   constexpr int kGroups = 256 / 16;
-  __shared__ float part[kTokSlots];  // [slot * S + s]: slots * S <= 32
+  __shared__ float part[ROWS * kTokSlots];  // [(rr * slots + slot) * S + s]: items <= ROWS * 32
   const int grp = threadIdx.x / 16, sub = threadIdx.x % 16;
   const int64_t K = q.Nout, N = q.Kred;
-  const int64_t row = blockIdx.x;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * ROWS;
   const int slots = static_cast<int>(q.n_tokens) * k;
-  const int S = slots >= kGroups ? 1 : (kGroups + slots - 1) / slots;
+  const int S = ROWS * slots >= kGroups ? 1 : (kGroups + ROWS * slots - 1) / (ROWS * slots);
   const int64_t slice = ((N / 8 + S - 1) / S) * 8;
   const uint16_t* __restrict__ w2 = reinterpret_cast<const uint16_t*>(q.B);
   const uint16_t* __restrict__ act = reinterpret_cast<const uint16_t*>(q.A);
-  for (int it = grp; it < slots * S; it += kGroups) {
-    const int f = it / S, sl = it - (it / S) * S;  // flat slot t * k + j, slice
+  for (int it = grp; it < ROWS * slots * S; it += kGroups) {
+    const int rs = it / S, sl = it - (it / S) * S;
+    const int rr = rs / slots, f = rs - (rs / slots) * slots;  // row in the block, flat slot t * k + j
+    const int64_t row = row0 + rr;
     const int e = q.tiny_ids[f];
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    if (e >= 0 && e < E) {
+    if (e >= 0 && e < E && row < K) {
       const uint16_t* wr = w2 + (static_cast<int64_t>(e) * K + row) * N;
       const uint16_t* ar = act + static_cast<int64_t>(f) * N;
       const int64_t n1 = min(N, (sl + 1) * slice);
@@ -1354,15 +1357,16 @@ __global__ __launch_bounds__(256) void gemm2_sum_token_kernel(GemmParams q, int 
     if (sub == 0) part[it] = v;
   }
   __syncthreads();
-  const int t = threadIdx.x;
-  if (t < q.n_tokens) {
+  const int rr = threadIdx.x / kTokSlots, t = threadIdx.x % kTokSlots;  // 256 / 32 = 8 >= ROWS
+  const int64_t row = row0 + rr;
+  if (rr < ROWS && t < q.n_tokens && row < K) {
     float y = 0.f;
     for (int j = 0; j < k; ++j) {
       const int f = t * k + j;
       const int e = q.tiny_ids[f];
       if (e < 0 || e >= E) continue;
       float d = 0.f;
-      for (int sl = 0; sl < S; ++sl) d += part[f * S + sl];
+      for (int sl = 0; sl < S; ++sl) d += part[(rr * slots + f) * S + sl];
       if (q.bias) d += q.bias[static_cast<int64_t>(e) * K + row];
       y += d * (q.gamma ? q.tiny_w[f] : 1.0f);
     }
@@ -1452,8 +1456,17 @@ int launch_gemm2_sum_token(const GemmParams& q, int E, int k, float scale, void*
     return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: M * k <= %d, N %% 8 == 0",
                            decode::kTokSlots);
   if (q.Nout > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: K too large");
-  decode::gemm2_sum_token_kernel<<<dim3(static_cast<unsigned>(q.Nout)), dim3(256), 0, s>>>(
-      q, E, k, scale, static_cast<uint16_t*>(out));
+  // 4 output rows per workgroup while that still leaves >= 512 workgroups
+  // (fewer, larger workgroups for short rows), else one row per workgroup
+#ifndef FMOE_TOK_G2_ROWS4_MIN_K
+#define FMOE_TOK_G2_ROWS4_MIN_K 2048
+#endif
+  if (q.Nout >= FMOE_TOK_G2_ROWS4_MIN_K && q.Nout % 4 == 0)
+    decode::gemm2_sum_token_kernel<4><<<dim3(static_cast<unsigned>(q.Nout / 4)), dim3(256), 0, s>>>(
+        q, E, k, scale, static_cast<uint16_t*>(out));
+  else
+    decode::gemm2_sum_token_kernel<1><<<dim3(static_cast<unsigned>(q.Nout)), dim3(256), 0, s>>>(
+        q, E, k, scale, static_cast<uint16_t*>(out));
   return fmoe_host::check_launch("gemm2_sum_token");
 }
 
