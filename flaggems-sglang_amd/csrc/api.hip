@@ -29,10 +29,7 @@ namespace {
 
 constexpr int kDecodeBM = 16;
 constexpr int kDecodeBN = 64;
-#ifndef FMOE_DECODE_TARGET_WGS
-#define FMOE_DECODE_TARGET_WGS 1024
-#endif
-constexpr int kDecodeTargetWgs = FMOE_DECODE_TARGET_WGS;
+constexpr int kDecodeTargetWgs = 1024;
 constexpr int kPrefillBN = 256;
 constexpr int kPrefillTargetWgs = 6 * 256;
 // at or above this many output tiles (2.5 waves of one workgroup per CU) the
@@ -129,6 +126,10 @@ extern "C" int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path)
   return choose_block_m(wtype, M, k, E, path);
 }
 
+extern "C" int fmoe_fused_block_m(int wtype, int64_t M, int k, int E, int path, int64_t K, int64_t N) {
+  return fit_block_m(wtype, choose_block_m(wtype, M, k, E, path), K, N);
+}
+
 extern "C" int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_routing* r, int path) {
   (void)path;
   if (!r) return 1;
@@ -147,10 +148,7 @@ extern "C" int fmoe_gemm2_splits(int wtype, int64_t K, int64_t N, const fmoe_rou
     // split than its extra prologue / epilogue and fp32 planes cost (reference
     // sweep M=1024 / 2048, 48 stages: unsplit 549 -> 504 / 854 -> 738 us;
     // Mixtral M=4096, 224 stages, keeps its 3 splits)
-#ifndef FMOE_PREFILL_MIN_SPLIT_STAGES
-#define FMOE_PREFILL_MIN_SPLIT_STAGES 64
-#endif
-    constexpr int64_t kMinStages = FMOE_PREFILL_MIN_SPLIT_STAGES;
+    constexpr int64_t kMinStages = 64;
     const int64_t max_sp = N / stage_elems / kMinStages > 1 ? N / stage_elems / kMinStages : 1;
     if (sp > max_sp) sp = max_sp;
     if (sp > 4) sp = 4;
@@ -380,12 +378,12 @@ int check_fused(const fmoe_fused_args* a) {
 // the intermediate per workgroup) plus the plane sum.  Its N / 128 fp32
 // partial planes per slot grow with M, so larger batches keep the two GEMM
 // launches.
-#ifndef FMOE_FUSED_INT4_MAX_M
-#define FMOE_FUSED_INT4_MAX_M 1
-#endif
+// (The kernel applies no bias; calls with b13 / b2 take the two-launch route.)
+constexpr int64_t kFusedInt4MaxM = 1;
 bool fused_int4_route(const fmoe_fused_args* a, int bm) {
   return a->wtype == FMOE_W_INT4_TILED && bm == kDecodeBM && a->activation != FMOE_ACT_SWIGLU &&
-         a->M <= FMOE_FUSED_INT4_MAX_M && a->top_k <= 32 && fused_int4_fits(a->M * a->top_k, a->K);
+         !a->b13 && !a->b2 && a->M <= kFusedInt4MaxM && a->top_k <= 32 &&
+         fused_int4_fits(a->M * a->top_k, a->K);
 }
 
 FusedLayout layout(const fmoe_fused_args* a) {
@@ -443,10 +441,7 @@ FusedLayout layout(const fmoe_fused_args* a) {
 // tiles let the GEMM workgroups start without the routing latency); MXFP4
 // never (measured slower).
 bool tiny_decode(const fmoe_fused_args* a, const FusedLayout& L) {
-#ifndef FMOE_TINY_INT4_MAX_M
-#define FMOE_TINY_INT4_MAX_M 1
-#endif
-  const int64_t max_m = is_int4(a->wtype) ? FMOE_TINY_INT4_MAX_M : (is_mx(a->wtype) ? 0 : 16);
+  const int64_t max_m = is_int4(a->wtype) ? 1 : (is_mx(a->wtype) ? 0 : 16);
   return L.bm == kDecodeBM && a->M <= max_m && a->M * a->top_k <= 512 && a->E <= 1024 &&
          !a->expert_map;
 }
@@ -506,23 +501,14 @@ int fused_tiny(const fmoe_fused_args* a, const FusedLayout& L, char* ws, hipStre
     return moe_sum_planes(y, L.splits, nullptr, a->topk_ids, a->E, a->M, a->top_k, a->K,
                           a->routed_scaling_factor, a->out, s);
   }
-#ifndef FMOE_TOKEN_G1
-#define FMOE_TOKEN_G1 1
-#endif
   // one bf16 token: GEMM1 as a row-parallel dot (more workgroups than 64-row blocks)
-  if (FMOE_TOKEN_G1 && a->M == 1 && a->wtype == FMOE_W_BF16) {
+  if (a->M == 1 && a->wtype == FMOE_W_BF16) {
     if (int st = launch_gemm1_token(g1, a->E, a->top_k, s)) return st;
   } else if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm1Silu, g1, s)) {
     return st;
   }
-#ifndef FMOE_TOKEN_SUM
-#define FMOE_TOKEN_SUM 1
-#endif
-#ifndef FMOE_TOKEN_SUM_MAX_M
-#define FMOE_TOKEN_SUM_MAX_M 1
-#endif
-  // small bf16 batches: GEMM2 and the top-k sum in one launch
-  if (FMOE_TOKEN_SUM && a->M <= FMOE_TOKEN_SUM_MAX_M && a->wtype == FMOE_W_BF16 && a->M * a->top_k <= 32)
+  // one bf16 token: GEMM2 and the top-k sum in one launch
+  if (a->M == 1 && a->wtype == FMOE_W_BF16 && a->M * a->top_k <= 32)
     return launch_gemm2_sum_token(g2, a->E, a->top_k, a->routed_scaling_factor, a->out, s);
   if (int st = launch_decode(to_wt(a->wtype), Mode::kGemm2, g2, s)) return st;
   return moe_sum_flat(y, L.splits, a->topk_ids, a->E, a->M, a->top_k, a->K, a->routed_scaling_factor,

@@ -96,15 +96,8 @@ struct Stage<WType::kMxfp4> {
 // the align launch, e.g. DSV3 M = 128, one stage and twice the occupancy is
 // 7% faster.  MXFP4: two, 3-5% faster at M = 16 (its e2m1 conversions hide
 // the second stage), even at M = 1.  bf16 / int4: one.)
-#ifndef FMOE_DECODE_PIPE_INT4
-#define FMOE_DECODE_PIPE_INT4 1
-#endif
-#ifndef FMOE_DECODE_ROTATE_INT4
-#define FMOE_DECODE_ROTATE_INT4 1
-#endif
-constexpr bool kRotateInt4 = FMOE_DECODE_ROTATE_INT4 != 0;
 constexpr int pipe_depth(WType wt, Mode mode, bool tiny) {
-  if (wt == WType::kInt4) return FMOE_DECODE_PIPE_INT4;
+  if (wt == WType::kInt4) return 1;
   return (wt == WType::kFp8 && mode == Mode::kGemm1Silu && tiny) || wt == WType::kMxfp4 ? 2 : 1;
 }
 
@@ -204,7 +197,7 @@ __device__ bool tiny_route(const GemmParams& p, int mt, TinyLds& L) {
 }
 
 template <WType WT, Mode MODE, int PIPE, int ACT, bool TINY, int RB>
-__global__ __launch_bounds__(kThreads * RB, (WT == WType::kInt4 && PIPE == 1 && kRotateInt4) ? 4 : 1) void gemm_decode_kernel(GemmParams p) {
+__global__ __launch_bounds__(kThreads * RB, WT == WType::kInt4 ? 4 : 1) void gemm_decode_kernel(GemmParams p) {
   __shared__ f32x4_t red[RB][kWaves][NI][kWave];
   __shared__ TinyLds tiny_lds[1];  // used by the TINY variant only
   const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
@@ -445,46 +438,8 @@ __global__ __launch_bounds__(kThreads * RB, (WT == WType::kInt4 && PIPE == 1 && 
                                                            as_bf16x8(b0, b1, b2, b3), acc[j], 0, 0, 0);
         }
       }
-    } else {  // int4
-      f32x4_t t[NI], xs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < NI; ++j) t[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
-      // 8 consecutive activations of nibble dword d occupy S.a[d]:
-      // (x0x1)(x2x3)(x4x5)(x6x7) -> reorder to (x0x4)(x1x5)(x2x6)(x3x7)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const int x01 = S.a[d][0], x23 = S.a[d][1], x45 = S.a[d][2], x67 = S.a[d][3];
-        const int p04 = __builtin_amdgcn_perm(x45, x01, 0x05040100);
-        const int p15 = __builtin_amdgcn_perm(x45, x01, 0x07060302);
-        const int p26 = __builtin_amdgcn_perm(x67, x23, 0x05040100);
-        const int p37 = __builtin_amdgcn_perm(x67, x23, 0x07060302);
-        const bf16x8_t a = as_bf16x8(p04, p15, p26, p37);
-        xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs, 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const unsigned wv = static_cast<unsigned>(S.b[j][d]);
-          const int b0 = static_cast<int>((wv & 0x000f000fu) | 0x43004300u);
-          const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
-          const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
-          const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
-          t[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, as_bf16x8(b0, b1, b2, b3), t[j], 0, 0, 0);
-        }
-      }
-      // fold zero and scale of group kt for this lane's column (row r of
-      // block j: scale half r % 2 of lane 8 j + r / 2's dword, zero nibble
-      // r % 8 of lane 32 + 2 j + r / 8's dword)
-      const int r16 = lane & 15;
-#pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        const unsigned sw = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), S.meta));
-        const unsigned zw = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), S.meta));
-        const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw >> 16) : (sw & 0xffffu))));
-        const float z = static_cast<float>((zw >> (4 * (r16 & 7))) & 15u);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[j][r] - (128.0f + z) * xs[r]);
-      }
     }
+    // (int4 stages are consumed inline by the main loop below)
   };
 
   // split-K range over stages, then interleaved over the 4 waves, PIPE
@@ -510,7 +465,7 @@ __global__ __launch_bounds__(kThreads * RB, (WT == WType::kInt4 && PIPE == 1 && 
       if constexpr (decode_prio<WT>() > 0) __builtin_amdgcn_s_setprio(0);
       kt = k2;
     }
-  } else if constexpr (WT == WType::kInt4 && kRotateInt4) {
+  } else if constexpr (WT == WType::kInt4) {
     // One stage of registers, reloaded piecewise as soon as each piece has
     // been consumed: the scale / zero dword right after it is spread with
     // ds_bpermute, each weight row block right after its MFMAs, the
@@ -641,10 +596,7 @@ __global__ __launch_bounds__(kThreads * RB, (WT == WType::kInt4 && PIPE == 1 && 
 // LDS ring published by one barrier per stage.  All global loads are ordinary
 // compiler-tracked loads.  Weights, scales / zeros and the arithmetic are the
 // row-block kernel's (one stage of weight registers reloaded piecewise).
-#ifndef FMOE_DECODE_RS_BLOCKS
-#define FMOE_DECODE_RS_BLOCKS 4
-#endif
-constexpr int kRsBlocks = FMOE_DECODE_RS_BLOCKS;  // row blocks (= waves) per workgroup
+constexpr int kRsBlocks = 4;  // row blocks (= waves) per workgroup
 constexpr int kRsThreads = 64 * kRsBlocks;
 constexpr int kRsPieces = 4 / kRsBlocks;          // activation loads per lane and stage
 static_assert(kRsBlocks == 1 || kRsBlocks == 2 || kRsBlocks == 4, "row blocks per workgroup");
@@ -882,10 +834,7 @@ constexpr int kFzCols = 128;                      // act columns per workgroup
 constexpr int kFzRowBlocks = kFzCols / (BN / 2);  // GEMM1 64-row blocks per workgroup
 constexpr int kFzKw = kFzWaves / kFzRowBlocks;    // waves per row block
 constexpr int kFzPitch = 2 * kFzCols + 16;        // LDS bytes per act row (padded)
-#ifndef FMOE_FUSED_INT4_BATCH
-#define FMOE_FUSED_INT4_BATCH 4
-#endif
-constexpr int kFzBatch = FMOE_FUSED_INT4_BATCH;   // w2 16-row groups per load batch
+constexpr int kFzBatch = 4;   // w2 16-row groups per load batch
 constexpr int kFzBatchRows = 16 * kFzBatch;
 static_assert(kFzBatch == 4 || kFzBatch == 8, "w2 batch: 64 or 128 rows");
 static_assert(kFzKw == kWaves && kFzRowBlocks == 4, "fused int4 geometry");
@@ -1169,26 +1118,8 @@ __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p,
 
 }  // namespace decode
 
-// Row blocks per workgroup by format and GEMM (build-time overridable for
-// measurements).
-#ifndef FMOE_DECODE_RB_BF16
-#define FMOE_DECODE_RB_BF16 1
-#endif
-#ifndef FMOE_DECODE_RB_FP8
-#define FMOE_DECODE_RB_FP8 2
-#endif
-#ifndef FMOE_DECODE_RB_INT4
-#define FMOE_DECODE_RB_INT4 1
-#endif
-#ifndef FMOE_DECODE_RB_MXFP4
-#define FMOE_DECODE_RB_MXFP4 1
-#endif
-constexpr int decode_row_blocks(WType wt) {
-  return wt == WType::kBf16 ? FMOE_DECODE_RB_BF16
-         : wt == WType::kFp8 ? FMOE_DECODE_RB_FP8
-         : wt == WType::kInt4 ? FMOE_DECODE_RB_INT4
-                              : FMOE_DECODE_RB_MXFP4;
-}
+// Row blocks per workgroup by format (measured: two for fp8, one otherwise).
+constexpr int decode_row_blocks(WType wt) { return wt == WType::kFp8 ? 2 : 1; }
 static_assert(decode_row_blocks(WType::kBf16) >= 1 && decode_row_blocks(WType::kBf16) <= decode::kMaxRB &&
                   decode_row_blocks(WType::kFp8) >= 1 && decode_row_blocks(WType::kFp8) <= decode::kMaxRB &&
                   decode_row_blocks(WType::kInt4) >= 1 && decode_row_blocks(WType::kInt4) <= decode::kMaxRB &&
@@ -1199,14 +1130,11 @@ static_assert(decode_row_blocks(WType::kBf16) >= 1 && decode_row_blocks(WType::k
 // activation stage per workgroup) instead of the row-block kernel.  Measured
 // on Mixtral W4A16 (tiled): M=64 (15 tiles) 254 -> 244 us; at M=4 / 16 (<= 9
 // tiles) its 4x coarser workgroups balance worse: 13% / 5% slower there.
-#ifndef FMOE_DECODE_INT4_RS
-#define FMOE_DECODE_INT4_RS 1
-#endif
 constexpr int kRsMinTiles = 14;
 // row blocks per workgroup of the int4 row-split kernel for a grid of
 // max_tiles expert tiles, 0 when the row-block kernel runs
 int decode_int4_row_split(int64_t max_tiles) {
-  return FMOE_DECODE_INT4_RS != 0 && max_tiles >= kRsMinTiles ? decode::kRsBlocks : 0;
+  return max_tiles >= kRsMinTiles ? decode::kRsBlocks : 0;
 }
 
 // Whether a call with `slots` top-k slots and hidden size K fits the one-launch
@@ -1458,10 +1386,7 @@ int launch_gemm2_sum_token(const GemmParams& q, int E, int k, float scale, void*
   if (q.Nout > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "gemm2_sum_token: K too large");
   // 4 output rows per workgroup while that still leaves >= 512 workgroups
   // (fewer, larger workgroups for short rows), else one row per workgroup
-#ifndef FMOE_TOK_G2_ROWS4_MIN_K
-#define FMOE_TOK_G2_ROWS4_MIN_K 2048
-#endif
-  if (q.Nout >= FMOE_TOK_G2_ROWS4_MIN_K && q.Nout % 4 == 0)
+  if (q.Nout >= 2048 && q.Nout % 4 == 0)
     decode::gemm2_sum_token_kernel<4><<<dim3(static_cast<unsigned>(q.Nout / 4)), dim3(256), 0, s>>>(
         q, E, k, scale, static_cast<uint16_t*>(out));
   else

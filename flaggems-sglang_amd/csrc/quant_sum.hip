@@ -370,10 +370,7 @@ int moe_sum_flat(const float* y, int splits, const int32_t* ids, int E, int64_t 
 // moe_sum over one plane of bf16 y rows (prefill GEMM2 without split-K).
 int moe_sum_bf16(const uint16_t* y, const int32_t* gate_indx, int64_t M, int k, int64_t K,
                  float scale, void* out, hipStream_t s) {
-#ifndef FMOE_SUM_ROWS
-#define FMOE_SUM_ROWS 1
-#endif
-  if (FMOE_SUM_ROWS && k <= kWave && K % 8 == 0) {
+  if (k <= kWave && K % 8 == 0) {
     const dim3 g(static_cast<unsigned>((M + 3) / 4)), b(256);
     moe_sum_rows_bf16_kernel<<<g, b, 0, s>>>(y, gate_indx, M, k, K, scale, static_cast<uint16_t*>(out));
     return check_launch("moe_sum_rows");

@@ -94,6 +94,8 @@ _SIGS = {
     "fmoe_gemm2_splits": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
                                          ctypes.POINTER(Routing), ctypes.c_int]),
     "fmoe_choose_block_m": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "fmoe_fused_block_m": (ctypes.c_int, [ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int64, ctypes.c_int64]),
     "fmoe_moe_sum": (ctypes.c_int, [vp, ctypes.c_int, vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
                                     ctypes.c_float, vp, vp]),
     "fmoe_fused_experts_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(FusedArgs)]),

@@ -178,11 +178,9 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int, num_experts: i
 
 
 def _block_m(wtype: int, M: int, k: int, E: int, path: int, K: int, N: int) -> int:
-    """The fused path's tile height (fmoe_choose_block_m), with 160-row fp8
-    tiles replaced by 128-row ones when K or N exceeds 8192 (the 160-row fp8
-    kernel stages the weight scales of at most 64 reduction blocks)."""
-    bm = lib().fmoe_choose_block_m(wtype, M, k, E, path)
-    return 128 if wtype == W_FP8 and bm == 160 and max(K, N) > 8192 else bm
+    """The fused path's tile height for a K x N layer (fmoe_fused_block_m: the
+    library's own choice, so stage-path routing always matches it)."""
+    return lib().fmoe_fused_block_m(wtype, M, k, E, path, K, N)
 
 
 def _standard_topk_to_triton_kernels(topk_weights, topk_ids, n_expts_tot, block_m: Optional[int] = None):

@@ -254,6 +254,13 @@ int fmoe_gemm2_ex(int wtype, const void* act, const float* act_scale, const void
  * their large-batch route dequantizes to bf16 inside fmoe_fused_experts). */
 int fmoe_choose_block_m(int wtype, int64_t M, int k, int E, int path);
 
+/* The tile height fmoe_fused_experts uses for a layer of hidden size K and
+ * intermediate size N: fmoe_choose_block_m with the fp8 160 -> 128 substitution
+ * above applied (callers that build their own routing for the stage API use
+ * this, so they always agree with the fused path).  Reference counterpart: the
+ * block size triton_kernels' matmul_ogs picks for its routing, ops/fused_moe.py:190. */
+int fmoe_fused_block_m(int wtype, int64_t M, int k, int E, int path, int64_t K, int64_t N);
+
 /* Top-k combine (the scatter + sum inside matmul_ogs, ops/fused_moe.py:208-216,
  * and routed_scaling_factor, :399-404): out[t, :] = bf16(scale *
  * sum_{j<k} sum_{p<splits} y[p][gate_indx[t*k + j], :]), summed in fixed

@@ -53,6 +53,11 @@ def test_host_queries():
     assert L.fmoe_choose_block_m(_lib.W_FP8, 8192, 8, 256, 0) == 160
     assert L.fmoe_choose_block_m(_lib.W_FP8, 3072, 8, 256, 0) == 128
     assert L.fmoe_choose_block_m(_lib.W_FP8, 6400, 8, 256, 0) == 128
+    # the fused path's choice: fp8 160-row tiles only while K, N <= 8192
+    assert L.fmoe_fused_block_m(_lib.W_FP8, 4096, 8, 256, 0, 7168, 2048) == 160
+    assert L.fmoe_fused_block_m(_lib.W_FP8, 4096, 8, 256, 0, 8448, 2048) == 128
+    assert L.fmoe_fused_block_m(_lib.W_FP8, 4096, 8, 256, 0, 7168, 8320) == 128
+    assert L.fmoe_fused_block_m(_lib.W_BF16, 1024, 8, 64, 0, 16384, 16384) == 160
 
 
 def test_argument_errors_map_to_reference_convention():

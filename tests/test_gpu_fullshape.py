@@ -3,7 +3,7 @@
 Where the CPU oracle finishes in seconds the whole output is compared
 (DeepSeek-V3 fp8 at E=256 for M = 1 and 128 -- the oracle dequantizes only
 the experts the tokens hit; Mixtral bf16 at M = 1 and 256).  At the large
-prefill sizes (DeepSeek-V3 fp8 M=4096, Qwen3 bf16 M=8192) the checks are the
+prefill sizes (DeepSeek-V3 fp8 M=4096 and 8192, Qwen3 bf16 M=8192) the checks are the
 size-independent ones: bit identity across runs, exact token-permutation
 equivariance, and an 8-token spot check against the oracle.
 
@@ -114,8 +114,9 @@ def _permutation_checks(call, oracle, x, tw, ti, tol, seed):
     _close(a[sel], oracle(x[sel], tw[sel], ti[sel]), tol)
 
 
-def test_dsv3_fp8_m4096_permutation_and_determinism(dsv3_layer):
-    x, tw, ti = _dsv3_routing(4096, seed=4096)
+@pytest.mark.parametrize("M", [4096, 8192])
+def test_dsv3_fp8_prefill_permutation_and_determinism(dsv3_layer, M):
+    x, tw, ti = _dsv3_routing(M, seed=M)
     _permutation_checks(lambda *a: _dsv3_call(dsv3_layer, *a),
                         lambda *a: _dsv3_oracle(dsv3_layer, *a), x, tw, ti, 5e-2, seed=9)
 

@@ -152,7 +152,7 @@ def _bf16_case(M, K, N, E, k, bias=0.0, seed=None):
     _close_literal(out, ref, 2e-2)
 
 
-@pytest.mark.parametrize("M", [1, 16, 256])
+@pytest.mark.parametrize("M", [1, 16, 64, 256, 1024])
 def test_qwen3_skewed_bf16(M):
     # E=128 top-8 K=2048 N=768, per-expert bias N(0, 0.5) skews the routing
     _bf16_case(M, 2048, 768, 128, 8, bias=0.5)
@@ -243,6 +243,13 @@ def test_mixtral_w4a16(M):
                                 z2.cpu(), d["topk_weights"], d["topk_ids"])
     _close(out, ref, 5e-2)
     _close_literal(out, ref, 5e-2)
+    # the tiled layout (the one serving loads by default) at the same full shape
+    outt = flaggems_sglang.fused_experts(d["x"].to(DEV), Q.tile_int4(q1), Q.tile_int4(q2),
+                                         d["topk_weights"].to(DEV), d["topk_ids"].to(DEV),
+                                         use_int4_w4a16=True, w1_scale=sc1, w2_scale=sc2, w1_zp=z1,
+                                         w2_zp=z2)
+    _close(outt, ref, 5e-2)
+    _close_literal(outt, ref, 5e-2)
 
 
 def test_product_quantizers_match_oracle():

@@ -299,3 +299,39 @@ def test_one_launch_decode_routing_paths_bit_exact():
     b = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, expert_map=emap, global_num_experts=E, **kw)
     _rel_below(a, b, 2e-3)
     assert not torch.equal(a, plain)
+
+
+@pytest.mark.gpu
+def test_tiled_m1_with_down_bias_takes_two_launch_route():
+    """A GEMM2 bias with SiLU is accepted by the C ABI; the one-launch kernel
+    applies no bias, so such single-token calls on tiled weights take the
+    two-launch route and match the row-major weights with the same bias."""
+    import flaggems_sglang  # noqa: F401
+    from flaggems_sglang import _lib
+    K, N, E, k = 512, 384, 8, 2
+    d, q1, q2, t1, t2, kw = _int4_layer(1, K, N, E, k)
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    b2 = (torch.randn(E, K, generator=torch.Generator().manual_seed(5)) * 0.5).to(DEV)
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run(wt, w13, w2, bias):
+        out = torch.empty(1, K, dtype=torch.bfloat16, device=DEV)
+        a = _lib.FusedArgs(wt, x.data_ptr(), 1, K, N, E, k, w13.data_ptr(), w2.data_ptr(),
+                           kw["w1_scale"].data_ptr(), kw["w2_scale"].data_ptr(), kw["w1_zp"].data_ptr(),
+                           kw["w2_zp"].data_ptr(), 128, tw.data_ptr(), ti.data_ptr(), 0, 1.0, 0,
+                           out.data_ptr(), None, 0, _lib.ACT_SILU, None, _lib.ptr(bias), 1.0, 0.0, None, 0)
+        n = L.fmoe_fused_experts_workspace_bytes(ctypes.byref(a))
+        ws = torch.empty(max(n, 1), dtype=torch.uint8, device=DEV)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), n
+        _lib.check(L.fmoe_fused_experts(ctypes.byref(a), st), "fused_experts")
+        torch.cuda.synchronize()
+        return out
+
+    tiled = run(_lib.W_INT4_TILED, t1, t2, b2)
+    rowm = run(_lib.W_INT4, q1, q2, b2)
+    assert torch.equal(tiled, rowm)  # same two-launch kernels, addresses only
+    plain = run(_lib.W_INT4_TILED, t1, t2, None)
+    # each slot adds its expert's bias row times its gate weight
+    want = plain.float() + sum(float(tw[0, j]) * b2[int(ti[0, j])] for j in range(k))
+    _rel_below(tiled, want, 1e-2)
