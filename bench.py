@@ -413,7 +413,7 @@ def _load_traffic(name):
         return None
 
 
-def measure(name, steps, warmup):
+def measure(name, steps, warmup, stages=True):
     import torch
 
     from flaggems_sglang import _lib
@@ -429,7 +429,10 @@ def measure(name, steps, warmup):
         timing = f"HIP graph of {n_layers} calls on distinct weight copies, per call"
     else:
         t = time_op(p, steps, warmup)
-    stages = stage_times(p)
+    if stages:
+        stages = stage_times(p)
+    else:  # profiling the fused path alone: no staged-path launches in the trace
+        stages = {"block_m": _lib.lib().fmoe_choose_block_m(wt, p["M"], p["k"], p["E"], 0)}
     f = flops(p)
     hit, wbytes = weight_bytes_touched(p)
     io_bytes = p["M"] * p["K"] * (2 if p["wtype"] != "fp8" else 1) + p["M"] * p["K"] * 2
@@ -443,6 +446,8 @@ def roofline_gemm1(res):
     """GEMM1+SiLU: algorithmic FLOPs 4*M*k*K*N per launch (bound mfma), or for
     decode the bytes of the touched w13 weights + x (bound hbm)."""
     p = res["p"]
+    if "gemm1" not in res["stages"]:
+        return None
     t = res["stages"]["gemm1"] * 1e-3
     decode = res["stages"]["block_m"] == 16
     if decode:
@@ -535,6 +540,9 @@ def main():
     ap.add_argument("--secondary", default=DEFAULT_SECONDARY,
                     help="comma list of extra workloads reported in 'secondary' ('' for none)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-stages", action="store_true",
+                    help="skip the staged-path stage timing (and the roofline computed from it), so a "
+                         "kernel trace holds the fused path's launches only")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a plain 1 GiB device copy 5x (reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -549,7 +557,7 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(2)
 
-    head = measure(args.workload, args.steps, args.warmup)
+    head = measure(args.workload, args.steps, args.warmup, stages=not args.no_stages)
     p = head["p"]
     line = {
         "metric": "fused_moe TFLOP/s & % MFMA peak (prefill); HBM GB/s % peak (decode), 1 GPU",
@@ -574,13 +582,14 @@ def main():
     }
     rl = roofline_gemm1(head)
     tr = _load_traffic(p["name"])
-    rl["traffic"] = None if tr is None else tr["bytes"]
-    if tr is not None:
-        rl["traffic_detail"] = {k: tr[k] for k in ("read_bytes", "write_bytes", "calibration", "source")}
+    if rl is not None:
+        rl["traffic"] = None if tr is None else tr["bytes"]
+        if tr is not None:
+            rl["traffic_detail"] = {k: tr[k] for k in ("read_bytes", "write_bytes", "calibration", "source")}
     line["roofline"] = rl
     sec = []
     for name in [s for s in args.secondary.split(",") if s and s != args.workload]:
-        r = measure(name, max(5, args.steps // 2), args.warmup)
+        r = measure(name, max(5, args.steps // 2), args.warmup, stages=not args.no_stages)
         e = secondary_entry(r)
         if name in CPU_SECONDARY and not args.no_cpu:
             e["cpu_baseline"] = cpu_baseline(r["p"], budget_s=6.0)

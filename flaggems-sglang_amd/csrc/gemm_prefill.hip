@@ -251,6 +251,14 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     row_end = t.row_end;
   }
 
+  // GEMM2: waves whose rows are all padding skip their fragment reads and
+  // MFMAs.  An expert's last M-tile is often nearly empty (Mixtral M=4096:
+  // ~1024 +- 30 slots per expert, so about half the experts add a fifth
+  // 256-row tile of a few dozen rows).  Measured: GEMM2 -0.5 to -1.5% on the
+  // BASELINE prefill shapes; GEMM1 +2-3% with the same skip, so not there.
+  const bool wave_live = C::WAVES_M == 1 || MODE == Mode::kGemm1Silu ||
+                         __builtin_amdgcn_readfirstlane(row_end - row_beg > wm * WM);
+
   const int64_t kbytes = FP8 ? p.Kred : p.Kred * 2;  // bytes per operand row
   const int nk_all = static_cast<int>(kbytes / SB);
   const int ksb = static_cast<int>(p.Kred / 128);      // fp8 scale blocks per row
@@ -291,7 +299,8 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       int64_t brow;
       if (MODE == Mode::kGemm1Silu) {
         const int w = r / WN, within = r % WN;
-        const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + w * (WN / 2) + (within % (WN / 2));
+        int64_t j = static_cast<int64_t>(nt) * (BN / 2) + w * (WN / 2) + (within % (WN / 2));
+        if (j >= p.N_act) j = p.N_act - 1;  // past the last column (BN / 2 need not divide N)
         brow = gemm1_row(ACT, p.N_act, j, within < WN / 2 ? 0 : 1);
       } else {
         brow = static_cast<int64_t>(nt) * BN + r;
@@ -452,7 +461,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
     else wait_ring<(C::UPW > 1 ? C::UPW - 1 : 1)>(newer);
     barrier_nofence();
     if (kt + NBUF - 1 < nk) issue(kt + NBUF - 1);
-    compute(kt);
+    if (wave_live) compute(kt);
   }
 
   // ---- epilogue.  C layout of a 16x16 block: lane holds column lane%16,
@@ -546,7 +555,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
           }
           w[c] = f32_to_bf16(a[0]) | (static_cast<uint32_t>(f32_to_bf16(a[1])) << 16);
         }
-        if (ok) *reinterpret_cast<uint2*>(act + col) = make_uint2(w[0], w[1]);
+        if (ok && col < p.N_act) *reinterpret_cast<uint2*>(act + col) = make_uint2(w[0], w[1]);
       }
     } else {
       float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
