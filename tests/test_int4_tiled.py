@@ -335,3 +335,19 @@ def test_tiled_m1_with_down_bias_takes_two_launch_route():
     # each slot adds its expert's bias row times its gate weight
     want = plain.float() + sum(float(tw[0, j]) * b2[int(ti[0, j])] for j in range(k))
     _rel_below(tiled, want, 1e-2)
+
+
+@pytest.mark.gpu
+def test_one_launch_regression_bits():
+    """The single-token tiled-int4 route against its stored output, bit for
+    bit (tests/golden/make_int4_regression.py): pins the plane order and the
+    rounding points that the tolerance checks above would let drift."""
+    import os
+    import sys
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    sys.path.insert(0, here)
+    import make_int4_regression as R
+    ref = np.load(os.path.join(here, R.NAME), allow_pickle=False)
+    sha, bits = R.run_case()
+    assert sha == str(ref["input_sha256"]), "seeded inputs drifted"
+    assert np.array_equal(bits, ref["out"])
