@@ -24,11 +24,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 }
 
 // fp32 -> bf16, round to nearest even (NaN kept quiet), as torch's .to(bfloat16).
+// Written as a select, not an early return: the compiler turns the early
+// return into a divergent branch per value (~15 exec-mask instructions), which
+// made the GEMM epilogues several times longer than their arithmetic.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }

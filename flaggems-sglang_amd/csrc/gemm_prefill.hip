@@ -530,11 +530,42 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       return;
     }
   }
+  // Routing weights of the lane's rows, loaded and waited for before the
+  // first store.  On gfx9 loads and stores share the vmcnt counter and the
+  // compiler treats them as completing out of order, so a use of a load that
+  // is still pending after a store waits for every store before it
+  // (vmcnt(0) at each of the tile's stores): the empty asm with the values as
+  // operands makes the compiler complete the loads here, once.
+  float gv[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int s = row_beg + wm * WM + i * 16 + orow;
+    gv[i] = (p.gamma && s < row_end) ? p.gate_scal[s] : 1.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i) asm volatile("" ::"v"(gv[i]));
+  // GEMM2 bias of the lane's columns (split 0 only), loaded the same way
+  float bv[MODE == Mode::kGemm2 ? NI : 1][4] = {};
+  if (MODE == Mode::kGemm2 && p.bias && split == 0) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + ocol;
+      if (col < p.Nout) {
+        const float* b = p.bias + static_cast<int64_t>(e) * p.Nout + col;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bv[j][c] = b[c];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(bv[j][c]));
+  }
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     const int s = row_beg + wm * WM + i * 16 + orow;
     const bool ok = s < row_end;
-    const float g = (p.gamma && ok) ? p.gate_scal[s] : 1.0f;
+    const float g = gv[i];
     if (MODE == Mode::kGemm1Silu) {
       uint16_t* act = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.N_act;
 #pragma unroll
@@ -565,10 +596,9 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
         f32x4_t v = acc[i][j];
         quad_transpose(v, lane);
         const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + ocol;
-        if (p.bias && split == 0 && col < p.Nout) {
-          const float* b = p.bias + static_cast<int64_t>(e) * p.Nout + col;
+        if (p.bias && split == 0) {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) v[c] += b[c];
+          for (int c = 0; c < 4; ++c) v[c] += bv[j][c];
         }
         if (ok && col < p.Nout) {
           if (p.y_bf16) {
