@@ -41,6 +41,8 @@
 //         The nibble pairs come out as k = (j, j+4) of each 8-nibble dword;
 //         the activations are permuted the same way with v_perm_b32.
 
+#include <type_traits>
+
 #include "gemm.hpp"
 
 namespace fmoe {
@@ -200,7 +202,11 @@ template <WType WT, Mode MODE, int PIPE, int ACT, bool TINY, int RB>
 __global__ __launch_bounds__(kThreads * RB, WT == WType::kInt4 ? 4 : 1) void gemm_decode_kernel(GemmParams p) {
   __shared__ f32x4_t red[RB][kWaves][NI][kWave];
   __shared__ TinyLds tiny_lds[1];  // used by the TINY variant only
-  const int tid = threadIdx.x, lane = tid % kWave, wid = tid / kWave;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  // wave index as a scalar: the compiler then treats the per-wave stage
+  // schedule (kw, k ranges, "more" stages) as uniform, so its loads sit under
+  // scalar branches and the waits before their uses count exactly
+  const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int kw = wid % kWaves;  // reduction-dim slice of this wave
   const int rb = wid / kWaves;  // row block of this wave
   int mt = blockIdx.x, ntw = blockIdx.y, split = blockIdx.z;
@@ -482,9 +488,13 @@ __global__ __launch_bounds__(kThreads * RB, WT == WType::kInt4 ? 4 : 1) void gem
     if (kt < k_end) load(kt, S);
     const int r16 = lane & 15;
     const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
-    for (; kt < k_end; kt += kWaves) {
+    // One step: consume stage kt, reloading the next stage's pieces as they
+    // free up (MORE) or not (the last step).  Peeled so that no load sits
+    // under a branch: the compiler then counts the loads exactly, and a
+    // step's first ds_bpermute waits only for the scale / zero dword.
+    auto step = [&](auto more_tag) {
+      constexpr bool MORE = decltype(more_tag)::value;
       if constexpr (decode_prio<WT>() > 0) __builtin_amdgcn_s_setprio(decode_prio<WT>());
-      const bool more = kt + kWaves < k_end;
       ap += a_step;
       mp += kWaves * meta_stride;
       woff += w_step;
@@ -494,7 +504,9 @@ __global__ __launch_bounds__(kThreads * RB, WT == WType::kInt4 ? 4 : 1) void gem
         sw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), S.meta));
         zw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), S.meta));
       }
-      if (more && lane < 40) S.meta = *reinterpret_cast<const int*>(mp);
+      // every lane loads (lanes 40-63 repeat a valid zero dword that no
+      // ds_bpermute reads)
+      if constexpr (MORE) S.meta = *reinterpret_cast<const int*>(mp);
       // activations of nibble dword d, permuted to the (j, j+4) pairing
       bf16x8_t a[4];
       f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
@@ -504,6 +516,15 @@ __global__ __launch_bounds__(kThreads * RB, WT == WType::kInt4 ? 4 : 1) void gem
         a[d] = as_bf16x8(__builtin_amdgcn_perm(x45, x01, 0x05040100), __builtin_amdgcn_perm(x45, x01, 0x07060302),
                          __builtin_amdgcn_perm(x67, x23, 0x05040100), __builtin_amdgcn_perm(x67, x23, 0x07060302));
         xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], ones, xs, 0, 0, 0);
+      }
+      // tiled weights: the next stage's activations (its first use) as soon
+      // as the registers are free, then its weights block by block below;
+      // row-major weights: the activations last (measured faster there)
+      if constexpr (MORE) {
+        if (tiled) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+        }
       }
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
@@ -517,18 +538,22 @@ __global__ __launch_bounds__(kThreads * RB, WT == WType::kInt4 ? 4 : 1) void gem
           const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
           t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
         }
-        if (more) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+        if constexpr (MORE) S.b[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
         const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw[j] >> 16) : (sw[j] & 0xffffu))));
         const float z = static_cast<float>((zw[j] >> (4 * (r16 & 7))) & 15u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[r] - (128.0f + z) * xs[r]);
       }
-      if (more) {
+      if constexpr (MORE) {
+        if (!tiled) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+          for (int q = 0; q < 4; ++q) S.a[q] = *reinterpret_cast<const i32x4_t*>(ap + 16 * q);
+        }
       }
       if constexpr (decode_prio<WT>() > 0) __builtin_amdgcn_s_setprio(0);
-    }
+    };
+    for (; kt + kWaves < k_end; kt += kWaves) step(std::true_type{});
+    if (kt < k_end) step(std::false_type{});
   } else {
     for (int kt = k_beg + kw; kt < k_end; kt += kWaves) {
       Stage<WT> s0;
