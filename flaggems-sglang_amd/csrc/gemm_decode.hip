@@ -743,11 +743,16 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
     }
 #pragma unroll
     for (int j = 0; j < NI; ++j) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
-    if (lane < 40) meta = *reinterpret_cast<const int*>(mp);
+    meta = *reinterpret_cast<const int*>(mp);  // every lane: see the row-block kernel
   }
   __syncthreads();
   const int r16 = lane & 15;
   const bf16x8_t ones = as_bf16x8(0x3f803f80, 0x3f803f80, 0x3f803f80, 0x3f803f80);
+  // Every global load of the loop is unconditional, the stage index clamped
+  // to the split's last stage (the last iterations re-read it: L2 hits):
+  // under a branch the compiler waited for all outstanding loads (the
+  // activation piece of stage kt + 2 included) before the first ds_bpermute.
+  const int k_last = k_beg + n - 1;
   for (int i = 0; i < n; ++i) {
     const int kt = k_beg + i;
     const bool more = i + 1 < n;
@@ -756,17 +761,21 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
 #pragma unroll
     for (int h = 0; h < kRsPieces; ++h) {
       if (more) *reinterpret_cast<i32x4_t*>(&a_lds[(i + 1) % 3][a_dst[h]]) = an[h];
-      if (i + 2 < n) an[h] = *reinterpret_cast<const i32x4_t*>(a_src[h] + static_cast<int64_t>(kt + 2) * 256);
+      an[h] = *reinterpret_cast<const i32x4_t*>(a_src[h] + static_cast<int64_t>(min(kt + 2, k_last)) * 256);
     }
-    woff += w_stride;
-    mp += meta_stride;
+    const int k1 = min(kt + 1, k_last);
+    woff = static_cast<int64_t>(k1) * w_stride;
+    mp = meta_ptr + k1 * meta_stride;
     unsigned sw[NI], zw[NI];
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
       sw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), meta));
       zw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), meta));
     }
-    if (more && lane < 40) meta = *reinterpret_cast<const int*>(mp);
+    // every lane loads (lanes 40-63 repeat a valid zero dword): under a
+    // lane-dependent branch the compiler waited for all outstanding loads,
+    // the activation piece of stage kt + 2 included, before the ds_bpermutes
+    meta = *reinterpret_cast<const int*>(mp);
     // activations of stage kt, permuted to the (j, j+4) nibble pairing
     const uint8_t* af = &a_lds[i % 3][a_frag];
     bf16x8_t a[4];
@@ -790,7 +799,7 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
         const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
         t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
       }
-      if (more) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
+      wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
       const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw[j] >> 16) : (sw[j] & 0xffffu))));
       const float z = static_cast<float>((zw[j] >> (4 * (r16 & 7))) & 15u);
 #pragma unroll
