@@ -471,6 +471,37 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   // scattered ones.
   const int orow = (lane >> 4) * 4 + (lane & 3);   // row within the 16x16 block
   const int ocol = ((lane >> 2) & 3) * 4;          // first of the lane's 4 columns
+  // Routing weights of the lane's rows, loaded and waited for before the
+  // first store.  On gfx9 loads and stores share the vmcnt counter and the
+  // compiler treats them as completing out of order, so a use of a load that
+  // is still pending after a store waits for every store before it
+  // (vmcnt(0) at each of the tile's stores): the empty asm with the values as
+  // operands makes the compiler complete the loads here, once.
+  float gv[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i) {
+    const int s = row_beg + wm * WM + i * 16 + orow;
+    gv[i] = (p.gamma && s < row_end) ? p.gate_scal[s] : 1.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < MI; ++i) asm volatile("" ::"v"(gv[i]));
+  // GEMM2 bias of the lane's columns (split 0 only), loaded the same way
+  float bv[MODE == Mode::kGemm2 ? NI : 1][4] = {};
+  if (MODE == Mode::kGemm2 && p.bias && split == 0) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + ocol;
+      if (col < p.Nout) {
+        const float* b = p.bias + static_cast<int64_t>(e) * p.Nout + col;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) bv[j][c] = b[c];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(bv[j][c]));
+  }
   if constexpr (FP8 && MODE == Mode::kGemm1Silu && BN / 2 == 128) {
     if (p.act_q) {
       // Activation quantized here, exactly as fmoe_quant_fp8_group would do
@@ -484,8 +515,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       float v[MI][NI / 2][4];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int s = row_beg + wm * WM + i * 16 + orow;
-        const float g = (p.gamma && s < row_end) ? p.gate_scal[s] : 1.0f;
+        const float g = gv[i];
         float amax = 0.f;
 #pragma unroll
         for (int j = 0; j < NI / 2; ++j) {
@@ -529,37 +559,6 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       }
       return;
     }
-  }
-  // Routing weights of the lane's rows, loaded and waited for before the
-  // first store.  On gfx9 loads and stores share the vmcnt counter and the
-  // compiler treats them as completing out of order, so a use of a load that
-  // is still pending after a store waits for every store before it
-  // (vmcnt(0) at each of the tile's stores): the empty asm with the values as
-  // operands makes the compiler complete the loads here, once.
-  float gv[MI];
-#pragma unroll
-  for (int i = 0; i < MI; ++i) {
-    const int s = row_beg + wm * WM + i * 16 + orow;
-    gv[i] = (p.gamma && s < row_end) ? p.gate_scal[s] : 1.0f;
-  }
-#pragma unroll
-  for (int i = 0; i < MI; ++i) asm volatile("" ::"v"(gv[i]));
-  // GEMM2 bias of the lane's columns (split 0 only), loaded the same way
-  float bv[MODE == Mode::kGemm2 ? NI : 1][4] = {};
-  if (MODE == Mode::kGemm2 && p.bias && split == 0) {
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-      const int64_t col = static_cast<int64_t>(nt) * BN + wn * WN + j * 16 + ocol;
-      if (col < p.Nout) {
-        const float* b = p.bias + static_cast<int64_t>(e) * p.Nout + col;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) bv[j][c] = b[c];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) asm volatile("" ::"v"(bv[j][c]));
   }
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
