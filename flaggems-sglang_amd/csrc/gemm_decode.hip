@@ -976,16 +976,18 @@ __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p,
       for (int j = 0; j < NI; ++j) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr0 + w_joff[j] + static_cast<int64_t>(kt) * 1024);
       meta = meta_at(kt);
     }
-    for (; kt < nk; kt += kFzKw) {
+    // peeled last step: no load sits under a branch, so the compiler's waits
+    // before the scale / zero ds_bpermutes and each weight block count exactly
+    auto step = [&](auto more_tag) {
+      constexpr bool MORE = decltype(more_tag)::value;
       const int kn = kt + kFzKw;
-      const bool more = kn < nk;
       unsigned sw[NI], zw[NI];
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         sw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (8 * j + (r16 >> 1)), meta));
         zw[j] = static_cast<unsigned>(__builtin_amdgcn_ds_bpermute(4 * (32 + 2 * j + (r16 >> 3)), meta));
       }
-      if (more) meta = meta_at(kn);
+      if constexpr (MORE) meta = meta_at(kn);
       bf16x8_t a[4];
       f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1007,17 +1009,19 @@ __global__ __launch_bounds__(kFzThreads, 1) void fused_int4_kernel(GemmParams p,
           const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
           t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
         }
-        if (more) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr0 + w_joff[j] + static_cast<int64_t>(kn) * 1024);
+        if constexpr (MORE) wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr0 + w_joff[j] + static_cast<int64_t>(kn) * 1024);
         const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw[j] >> 16) : (sw[j] & 0xffffu))));
         const float z = static_cast<float>((zw[j] >> (4 * (r16 & 7))) & 15u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[r] - (128.0f + z) * xs[r]);
       }
-      if (more) {
+      if constexpr (MORE) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) av[d] = *reinterpret_cast<const i32x4_t*>(&xr_lds[a_off + kn * 256 + 16 * d]);
       }
-    }
+    };
+    for (; kt + kFzKw < nk; kt += kFzKw) step(std::true_type{});
+    if (kt < nk) step(std::false_type{});
   }
 
   // ---- GEMM2 operands: the wave's row batches b = wid, wid + 16, ...;
