@@ -316,36 +316,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   const bool sa_lane = sa_wave && 64 * sa_j + lane < BM;
   const float* sa_src = nullptr;
   if (sa_wave) sa_src = p.a_scale + a_src_row(min(64 * sa_j + lane, BM - 1)) * ksb + k0;
-  // fp8 weight scales of the whole k range, staged once in LDS
   int sb_split = NI;  // GEMM2: 16-row blocks of the wave under its first weight-scale block
-  if (FP8) {
-    const int64_t nrb = p.Nout / 128;
-    const float* se = p.b_scale + static_cast<int64_t>(e) * nrb * ksb;
-    const float* s0;
-    const float* s1;
-    if (MODE == Mode::kGemm1Silu) {
-      // the wave's gate rows (and up rows) lie in one 128-row scale block
-      const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2);
-      s0 = se + (gemm1_row(ACT, p.N_act, j, 0) / 128) * ksb;
-      s1 = se + (gemm1_row(ACT, p.N_act, j, 1) / 128) * ksb;
-    } else {
-      // the wave's rows span at most two 128-row scale blocks (WN <= 128):
-      // 16-row blocks j < sb_split use the first one
-      int64_t j = static_cast<int64_t>(nt) * BN + wn * WN;
-      if (j >= p.Nout) j = p.Nout - 1;
-      const int64_t jl = min(j + WN - 1, p.Nout - 1);
-      s0 = se + (j / 128) * ksb;
-      s1 = se + (jl / 128) * ksb;
-      if (jl / 128 != j / 128) sb_split = static_cast<int>((128 - j % 128) / 16);
-    }
-    if (wm == 0)
-      for (int kk = lane; kk < nk; kk += kWave) {
-        sb_lds[wn][0][kk] = s0[k0 + kk];
-        sb_lds[wn][1][kk] = s1[k0 + kk];
-      }
-    __syncthreads();
-  }
-
   auto issue = [&](int kt) {
     uint8_t* st = lds[kt % NBUF];
     const int64_t off = static_cast<int64_t>(kt) * SB;
@@ -451,6 +422,36 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
 #pragma unroll
   for (int s = 0; s < NBUF - 1; ++s)
     if (s < nk) issue(s);
+  // fp8 weight scales of the whole k range, staged once in LDS -- after the
+  // first stages' DMA is issued, so the two round trips overlap
+  if (FP8) {
+    const int64_t nrb = p.Nout / 128;
+    const float* se = p.b_scale + static_cast<int64_t>(e) * nrb * ksb;
+    const float* s0;
+    const float* s1;
+    if (MODE == Mode::kGemm1Silu) {
+      // the wave's gate rows (and up rows) lie in one 128-row scale block
+      const int64_t j = static_cast<int64_t>(nt) * (BN / 2) + wn * (WN / 2);
+      s0 = se + (gemm1_row(ACT, p.N_act, j, 0) / 128) * ksb;
+      s1 = se + (gemm1_row(ACT, p.N_act, j, 1) / 128) * ksb;
+    } else {
+      // the wave's rows span at most two 128-row scale blocks (WN <= 128):
+      // 16-row blocks j < sb_split use the first one
+      int64_t j = static_cast<int64_t>(nt) * BN + wn * WN;
+      if (j >= p.Nout) j = p.Nout - 1;
+      const int64_t jl = min(j + WN - 1, p.Nout - 1);
+      s0 = se + (j / 128) * ksb;
+      s1 = se + (jl / 128) * ksb;
+      if (jl / 128 != j / 128) sb_split = static_cast<int>((128 - j % 128) / 16);
+    }
+    if (wm == 0)
+      for (int kk = lane; kk < nk; kk += kWave) {
+        sb_lds[wn][0][kk] = s0[k0 + kk];
+        sb_lds[wn][1][kk] = s1[k0 + kk];
+      }
+    __syncthreads();
+  }
+
   // DMA instructions per stage for this wave: UPW or UPW - 1 operand units,
   // plus one a-scale load
   const int per = (full_wave ? C::UPW : C::UPW - 1) + (sa_wave ? 1 : 0);
