@@ -615,21 +615,33 @@ __global__ __launch_bounds__(kThreads * RB, WT == WType::kInt4 ? 4 : 1) void gem
 
 // int4 decode, row split: the workgroup's 4 waves each own one 64-row block
 // of the weights over the whole reduction range (of this split), all on the
-// same stage at a time, so the tile's 16-slot activation stage (4 KiB) is
-// loaded once per workgroup instead of once per wave: each wave brings a
-// quarter of it (4 rows) two stages ahead, through registers into a 3-slot
-// LDS ring published by one barrier per stage.  All global loads are ordinary
-// compiler-tracked loads.  Weights, scales / zeros and the arithmetic are the
-// row-block kernel's (one stage of weight registers reloaded piecewise).
+// same stage at a time, so the activation stage is loaded once per workgroup
+// instead of once per wave: each wave brings a quarter of it two stages ahead,
+// through registers into a 3-slot LDS ring published by one barrier per
+// stage.  All global loads are ordinary compiler-tracked loads.  Weights,
+// scales / zeros and the arithmetic are the row-block kernel's (one stage of
+// weight registers reloaded piecewise).
+// PAIR: a workgroup takes a pair of the routing's 16-slot tiles, the
+// expert's tiles 2i and 2i + 1 (32 rows, 8 KiB of activations per stage), so
+// every weight fragment feeds two MFMA row halves and the workgroup of an odd
+// tile exits: an expert with 17-32 slots streams its weights once instead of
+// twice.  Padding rows re-read the tile's first row (coalesced with it by the
+// load instruction).  It needs ~160 VGPRs (3 waves per SIMD instead of 4), so
+// it is taken when the experts average >= 24 slots (Mixtral W4A16 M=256: 535
+// -> 450-465 µs; at M=64, ~16 +- 4 slots, the single tiles would pay the
+// second half and the occupancy: 3-5% slower).
 constexpr int kRsBlocks = 4;  // row blocks (= waves) per workgroup
 constexpr int kRsThreads = 64 * kRsBlocks;
-constexpr int kRsPieces = 4 / kRsBlocks;          // activation loads per lane and stage
 static_assert(kRsBlocks == 1 || kRsBlocks == 2 || kRsBlocks == 4, "row blocks per workgroup");
 constexpr int kRsPitch = 256 + 16;  // LDS bytes per activation row (padded against bank conflicts)
+constexpr int kRsPairMinSlots = 24;  // mean slots per expert from which tiles are paired
 
-template <Mode MODE, int ACT>
-__global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_rs_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t a_lds[3][BM * kRsPitch];
+template <Mode MODE, int ACT, bool PAIR>
+__global__ __launch_bounds__(kRsThreads, PAIR ? 2 : 16 / kRsBlocks) void gemm_decode_int4_rs_kernel(GemmParams p) {
+  constexpr int H = PAIR ? 2 : 1;                      // 16-row halves
+  constexpr int kRsRows = H * BM;                      // activation rows of the workgroup
+  constexpr int kRsPieces = kRsRows / (4 * kRsBlocks);  // activation loads per lane and stage
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[3][kRsRows * kRsPitch];
   const int tid = threadIdx.x, lane = tid % kWave;
   const int wid = __builtin_amdgcn_readfirstlane(tid / kWave);
   // workgroup -> (split, tile, group of 4 row blocks), XCD-contiguous as in
@@ -651,25 +663,26 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
   }
   const int nt = ntw * kRsBlocks + wid;  // this wave's 64-row block
   const int tm = p.tile_map[mt];
+  if (PAIR && ((tm >> 16) & 1)) return;  // the odd tile of a pair: computed with the even one
   const int e = tm & 0xffff;
   const int row_beg = p.offs_raw[e] + (tm >> 16) * BM;
-  const int n_rows = min(p.offs_raw[e + 1], row_beg + BM) - row_beg;
+  const int n_rows = min(p.offs_raw[e + 1], row_beg + kRsRows) - row_beg;
 
-  // activation rows: piece h of this lane is row 16 wid / kRsBlocks + 4 h +
-  // lane / 16 (16 bytes of its 256-byte stage slice); fragments are read as
-  // the row-block kernel loads them (lane -> row lane % 16, bytes 64 (lane /
-  // 16) .. + 63)
+  // activation rows: piece h of this lane is row (kRsRows / kRsBlocks) wid +
+  // 4 h + lane / 16 (16 bytes of its 256-byte stage slice); fragments are
+  // read as the row-block kernel loads them (lane -> row 16 half + lane % 16,
+  // bytes 64 (lane / 16) .. + 63)
   const uint8_t* a_src[kRsPieces];
   int a_dst[kRsPieces];
 #pragma unroll
   for (int h = 0; h < kRsPieces; ++h) {
-    const int ar = (16 / kRsBlocks) * wid + 4 * h + (lane >> 4);
+    const int ar = (kRsRows / kRsBlocks) * wid + 4 * h + (lane >> 4);
     const int as = row_beg + (ar < n_rows ? ar : 0);
     const int64_t a_row = MODE == Mode::kGemm1Silu ? p.topk_indx[as] / p.top_k : as;
     a_src[h] = p.A + a_row * p.Kred * 2 + (lane & 15) * 16;
     a_dst[h] = ar * kRsPitch + (lane & 15) * 16;
   }
-  const int a_frag = (lane & 15) * kRsPitch + (lane >> 4) * 64;
+  const int a_frag = (lane & 15) * kRsPitch + (lane >> 4) * 64;  // half 1: + 16 rows
 
   const int64_t w_bytes = p.Kred / 2;
   const int nk = static_cast<int>(p.Kred / 128);
@@ -722,9 +735,11 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
     }
   }
 
-  f32x4_t acc[NI];
+  f32x4_t acc[H][NI];
 #pragma unroll
-  for (int j = 0; j < NI; ++j) acc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int h = 0; h < H; ++h)
+#pragma unroll
+    for (int j = 0; j < NI; ++j) acc[h][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int per_split = (nk + p.splits - 1) / p.splits;
   const int k_beg = min(nk, split * per_split);
@@ -776,20 +791,27 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
     // lane-dependent branch the compiler waited for all outstanding loads,
     // the activation piece of stage kt + 2 included, before the ds_bpermutes
     meta = *reinterpret_cast<const int*>(mp);
-    // activations of stage kt, permuted to the (j, j+4) nibble pairing
-    const uint8_t* af = &a_lds[i % 3][a_frag];
-    bf16x8_t a[4];
-    f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+    // activations of stage kt for both row halves, permuted to the (j, j+4)
+    // nibble pairing
+    bf16x8_t a[H][4];
+    f32x4_t xs[H];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const i32x4_t v = *reinterpret_cast<const i32x4_t*>(af + 16 * d);
-      a[d] = as_bf16x8(__builtin_amdgcn_perm(v[2], v[0], 0x05040100), __builtin_amdgcn_perm(v[2], v[0], 0x07060302),
-                       __builtin_amdgcn_perm(v[3], v[1], 0x05040100), __builtin_amdgcn_perm(v[3], v[1], 0x07060302));
-      xs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], ones, xs, 0, 0, 0);
+    for (int h = 0; h < H; ++h) {
+      xs[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const uint8_t* af = &a_lds[i % 3][a_frag + 16 * h * kRsPitch];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const i32x4_t v = *reinterpret_cast<const i32x4_t*>(af + 16 * d);
+        a[h][d] = as_bf16x8(__builtin_amdgcn_perm(v[2], v[0], 0x05040100), __builtin_amdgcn_perm(v[2], v[0], 0x07060302),
+                            __builtin_amdgcn_perm(v[3], v[1], 0x05040100), __builtin_amdgcn_perm(v[3], v[1], 0x07060302));
+        xs[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[h][d], ones, xs[h], 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
-      f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t t[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) t[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const unsigned wv = static_cast<unsigned>(wb[j][d]);
@@ -797,23 +819,28 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
         const int b1 = static_cast<int>(((wv >> 4) & 0x000f000fu) | 0x43004300u);
         const int b2 = static_cast<int>(((wv >> 8) & 0x000f000fu) | 0x43004300u);
         const int b3 = static_cast<int>(((wv >> 12) & 0x000f000fu) | 0x43004300u);
-        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[d], as_bf16x8(b0, b1, b2, b3), t, 0, 0, 0);
+        const bf16x8_t bq = as_bf16x8(b0, b1, b2, b3);
+#pragma unroll
+        for (int h = 0; h < H; ++h) t[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[h][d], bq, t[h], 0, 0, 0);
       }
       wb[j] = *reinterpret_cast<const i32x4_t*>(w_ptr[j] + woff);
       const float sc = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>((r16 & 1) ? (sw[j] >> 16) : (sw[j] & 0xffffu))));
       const float z = static_cast<float>((zw[j] >> (4 * (r16 & 7))) & 15u);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[j][r] += sc * (t[r] - (128.0f + z) * xs[r]);
+      for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[h][j][r] += sc * (t[h][r] - (128.0f + z) * xs[h][r]);
     }
     __syncthreads();  // stage kt + 1 visible; stage kt's slot free from stage kt + 2 on
   }
 
-  // ---- epilogue: this wave's rows (the row-block kernel's, without the
-  // cross-wave reduction)
+  // ---- epilogue: this wave's rows of both halves (the row-block kernel's,
+  // without the cross-wave reduction)
   const int col16 = lane & 15;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int rr = (lane >> 4) * 4 + r;
+  for (int hr = 0; hr < 4 * H; ++hr) {
+    const int h = hr >> 2, r = hr & 3;
+    const int rr = 16 * h + (lane >> 4) * 4 + r;
     if (rr >= n_rows) continue;
     const int s = row_beg + rr;
     const float g = p.gamma ? p.gate_scal[s] : 1.0f;
@@ -825,7 +852,7 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
         if (col >= p.N_act) continue;
         float gb, ub;
         gemm1_bias<ACT>(p, e, col, gb, ub);
-        act[col] = f32_to_bf16(gemm1_act<ACT>(p, acc[j][r], acc[j + NI / 2][r], gb, ub, g));
+        act[col] = f32_to_bf16(gemm1_act<ACT>(p, acc[h][j][r], acc[h][j + NI / 2][r], gb, ub, g));
       }
     } else {
       float* y = static_cast<float*>(p.out) + split * p.out_split_stride + static_cast<int64_t>(s) * p.Nout;
@@ -834,7 +861,7 @@ __global__ __launch_bounds__(kRsThreads, 16 / kRsBlocks) void gemm_decode_int4_r
         const int64_t col = static_cast<int64_t>(nt) * BN + j * 16 + col16;
         if (col < p.Nout) {
           const float bb = (p.bias && split == 0) ? p.bias[static_cast<int64_t>(e) * p.Nout + col] : 0.f;
-          y[col] = (acc[j][r] + bb) * g;
+          y[col] = (acc[h][j][r] + bb) * g;
         }
       }
     }
@@ -1175,6 +1202,13 @@ int decode_int4_row_split(int64_t max_tiles) {
   return max_tiles >= kRsMinTiles ? decode::kRsBlocks : 0;
 }
 
+// Whether the row-split kernel pairs tiles: slots estimated from the tile
+// bound (max_tiles = E - 1 + ceil((slots - E + 1) / 16), so >= the slots / 16)
+bool decode_int4_pair(int64_t max_tiles, int E) {
+  const int64_t slots_est = (max_tiles - (E - 1)) * decode::BM;
+  return slots_est >= static_cast<int64_t>(decode::kRsPairMinSlots) * E;
+}
+
 // Whether a call with `slots` top-k slots and hidden size K fits the one-launch
 // int4 kernel's LDS staging of a tile's x rows (at most min(16, slots) rows).
 bool fused_int4_fits(int64_t slots, int64_t K) {
@@ -1217,14 +1251,25 @@ int launch_decode(WType wt, Mode mode, const GemmParams& p0, hipStream_t s) {
   if (wt == WType::kInt4 && !p.tiny_ids && decode_int4_row_split(p.max_tiles) > 0) {
     g.y = static_cast<unsigned>((nblocks + decode::kRsBlocks - 1) / decode::kRsBlocks);
     const dim3 b(decode::kRsThreads);
-    if (mode == Mode::kGemm2)
-      decode::gemm_decode_int4_rs_kernel<Mode::kGemm2, kActSilu><<<g, b, 0, s>>>(p);
-    else if (p.act == kActSwiglu)
-      decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSwiglu><<<g, b, 0, s>>>(p);
-    else if (p.act == kActGelu)
-      decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActGelu><<<g, b, 0, s>>>(p);
-    else
-      decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSilu><<<g, b, 0, s>>>(p);
+    if (decode_int4_pair(p.max_tiles, p.n_experts)) {
+      if (mode == Mode::kGemm2)
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm2, kActSilu, true><<<g, b, 0, s>>>(p);
+      else if (p.act == kActSwiglu)
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSwiglu, true><<<g, b, 0, s>>>(p);
+      else if (p.act == kActGelu)
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActGelu, true><<<g, b, 0, s>>>(p);
+      else
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSilu, true><<<g, b, 0, s>>>(p);
+    } else {
+      if (mode == Mode::kGemm2)
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm2, kActSilu, false><<<g, b, 0, s>>>(p);
+      else if (p.act == kActSwiglu)
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSwiglu, false><<<g, b, 0, s>>>(p);
+      else if (p.act == kActGelu)
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActGelu, false><<<g, b, 0, s>>>(p);
+      else
+        decode::gemm_decode_int4_rs_kernel<Mode::kGemm1Silu, kActSilu, false><<<g, b, 0, s>>>(p);
+    }
     return fmoe_host::check_launch("gemm_decode_int4_rs");
   }
 #define LAUNCH(WT_, MODE_, ACT_)                                                                      \

@@ -230,7 +230,7 @@ def test_bf16_160_row_tiles_skewed():
     _close(out2, ref, 2e-2)
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 64])
+@pytest.mark.parametrize("M", [1, 4, 16, 64, 256])  # 256: ~64 slots per expert, paired row-split tiles
 def test_mixtral_w4a16(M):
     K, N, E, k = 4096, 14336, 8, 2
     d = O.make_inputs(M, K, N, E, k, wscale=0.02)
