@@ -165,6 +165,43 @@ def test_fused_tiled_expert_map_and_no_combine():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("tiled", [False, True])
+def test_paired_row_split_odd_tiles_and_expert_map(tiled):
+    """int4 decode batches of >= 24 slots per expert take the row-split kernel
+    with paired 16-slot tiles (the workgroup of tile 2i computes 2i and 2i + 1,
+    the odd tile's workgroup exits).  Skewed routing gives experts an odd
+    number of tiles (a lone last tile) and experts of <= 16 slots (one tile,
+    the pair's second half empty); an expert map drops two experts.  Both
+    against the dequantizing oracle."""
+    import flaggems_sglang
+    from flaggems_sglang import quant as Q
+    from oracle import fused_moe_oracle as O
+    M, K, N, E, k = 300, 512, 384, 8, 2
+    d = O.make_inputs(M, K, N, E, k, wscale=0.05, expert_bias_std=1.0)
+    counts = torch.bincount(d["topk_ids"].flatten().long(), minlength=E)
+    tiles = (counts + 15) // 16
+    assert bool((tiles % 2 == 1).any()) and int(counts.min()) <= 16 and int(counts.max()) > 32, counts
+    q1, s1, z1 = Q.quantize_int4_group(d["w13"].to(DEV))
+    q2, s2, z2 = Q.quantize_int4_group(d["w2"].to(DEV))
+    kw = dict(use_int4_w4a16=True, w1_scale=s1, w2_scale=s2, w1_zp=z1, w2_zp=z2)
+    w1, w2 = (Q.tile_int4(q1), Q.tile_int4(q2)) if tiled else (q1, q2)
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+
+    def ref(tw_, ti_):
+        return O.fused_experts_w4a16(d["x"], q1.cpu(), s1.cpu(), z1.cpu(), q2.cpu(), s2.cpu(), z2.cpu(),
+                                     tw_, ti_)
+
+    out = flaggems_sglang.fused_experts(x, w1, w2, tw, ti, **kw)
+    _rel_below(out, ref(d["topk_weights"], d["topk_ids"]), 5e-2 / 4)
+    emap = torch.arange(E, dtype=torch.int32)
+    emap[1] = -1
+    emap[int(counts.argmax())] = -1
+    out = flaggems_sglang.fused_experts(x, w1, w2, tw, ti, expert_map=emap.to(DEV), global_num_experts=E, **kw)
+    ltw, lti = O.ep_localize(d["topk_weights"], d["topk_ids"], emap)
+    _rel_below(out, ref(ltw, lti), 5e-2 / 4)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("M,K,N,E,k", [(1, 512, 384, 8, 2), (16, 1024, 768, 8, 2), (300, 256, 512, 8, 2)])
 def test_fused_mxfp4_tiled_equals_row_major(M, K, N, E, k):
     import flaggems_sglang
