@@ -6,6 +6,7 @@
 
 namespace fmoe {
 int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t s);
+size_t prefill_tail_bytes(WType wt, int bm, int64_t max_tiles, int64_t Nout);
 int decode_int4_row_split(int64_t max_tiles);
 int launch_decode(WType wt, Mode mode, const GemmParams& p, hipStream_t s);
 int launch_gemm1_token(const GemmParams& p, int E, int k, hipStream_t s);
@@ -203,7 +204,8 @@ int gemm1_impl(int wtype, const void* x, const float* x_scale, const void* w13,
 int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w2,
                const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
                const fmoe_routing* r, int apply_gamma, const float* bias, void* y, int splits,
-               int path, int4* tile_lut, bool y_bf16, void* stream);
+               int path, int4* tile_lut, bool y_bf16, void* stream, float* tail_part = nullptr,
+               size_t tail_bytes = 0);
 }  // namespace
 
 extern "C" int fmoe_gemm1_ex(int wtype, const void* x, const float* x_scale, const void* w13,
@@ -293,7 +295,8 @@ namespace {
 int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w2,
                const void* w2_scale, const void* w2_zero, int64_t K, int64_t N,
                const fmoe_routing* r, int apply_gamma, const float* bias, void* y, int splits,
-               int path, int4* tile_lut, bool y_bf16, void* stream) {
+               int path, int4* tile_lut, bool y_bf16, void* stream, float* tail_part,
+               size_t tail_bytes) {
   if (int st = check_routing(r, "gemm2")) return st;
   if (!valid_wtype(wtype)) return fail(FMOE_ERR_INVALID, "gemm2: unknown weight type %d", wtype);
   if (K <= 0 || N <= 0 || K % 128 != 0 || N % 128 != 0)
@@ -335,6 +338,11 @@ int gemm2_impl(int wtype, const void* act, const float* act_scale, const void* w
   p.splits = splits;
   p.out_split_stride = r->n_tokens * r->top_k * K;
   p.tile_lut = tile_lut;
+  // fused prefill: tail split instead of split-K planes (the launcher turns
+  // it off when the buffer or the runtime's occupancy query falls short)
+  p.tail_split = (tail_part && !is_decode(r) && p.y_bf16) ? kTailMaxSplit : 0;
+  p.tail_part = tail_part;
+  p.tail_bytes = tail_bytes;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (is_decode(r)) return launch_decode(to_wt(wtype), Mode::kGemm2, p, s);
   return launch_prefill(to_wt(wtype), Mode::kGemm2, r->block_m, p, s);
@@ -351,7 +359,8 @@ struct FusedLayout {
   bool fused4;  // one-launch int4 decode (splits = N / 128 planes)
   int64_t max_tiles;
   size_t align_ws, expt_indx, expt_scal, topk_indx, gate_indx, gate_scal, hist, offs_raw,
-      offs_pad, tile_map, n_tiles, xq, xs, act, actq, acts, y, lut, total;
+      offs_pad, tile_map, n_tiles, xq, xs, act, actq, acts, y, lut, tail, total;
+  size_t tail_bytes;  // prefill GEMM2 tail-split partials (0: split-K planes or none)
 };
 
 int check_fused(const fmoe_fused_args* a) {
@@ -399,6 +408,18 @@ FusedLayout layout(const fmoe_fused_args* a) {
   r.max_tiles = static_cast<int32_t>(L.max_tiles);
   L.fused4 = fused_int4_route(a, L.bm);
   L.splits = L.fused4 ? static_cast<int>(a->N / 128) : fmoe_gemm2_splits(a->wtype, a->K, a->N, &r, 0);
+  // Prefill GEMM2 that the split rule would cut into fp32 planes (few tiles,
+  // a long reduction): whole tiles store bf16 rows instead and only the
+  // tiles of each XCD's last partial round are split (tail_fold_kernel adds
+  // their partials).  Mixtral M=4096: GEMM2 + sum 1027 -> 917 us.  Where the
+  // rule keeps whole tiles, splitting the last round lost (the split
+  // workgroups' prologue, fp32 stores and fold cost more than the idle
+  // slots: Qwen3 M=8192 GEMM2 351 -> 387 us, DSV3 M=4096 1107 -> 1158 us).
+  L.tail_bytes = (L.bm != kDecodeBM && !L.fused4 && L.splits > 1 &&
+                  (a->wtype == FMOE_W_BF16 || a->wtype == FMOE_W_FP8))
+                     ? prefill_tail_bytes(to_wt(a->wtype), L.bm, L.max_tiles, a->K)
+                     : 0;
+  if (L.tail_bytes > 0) L.splits = 1;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     size_t o = off;
@@ -429,6 +450,7 @@ FusedLayout layout(const fmoe_fused_args* a) {
   const int64_t nn1 = (a->N + kPrefillBN / 2 - 1) / (kPrefillBN / 2);
   const int64_t nn2 = (a->K + kPrefillBN - 1) / kPrefillBN;
   L.lut = take(L.bm == kDecodeBM ? 0 : 16 * static_cast<size_t>(L.max_tiles) * (nn1 > nn2 ? nn1 : nn2));
+  L.tail = take(L.tail_bytes);
   L.total = off;
   return L;
 }
@@ -665,7 +687,8 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
   // split-K planes and the decode path stay fp32.
   if (int st = gemm2_impl(a->wtype, act, acts, a->w2, a->w2_scale, a->w2_zero, a->K, a->N, &r,
                           !a->apply_router_weight_on_input, a->b2, at(L.y), L.splits, 0, lut,
-                          L.y_bf16, stream))
+                          L.y_bf16, stream, L.tail_bytes ? static_cast<float*>(at(L.tail)) : nullptr,
+                          L.tail_bytes))
     return st;
   if (L.y_bf16)
     return moe_sum_bf16(static_cast<const uint16_t*>(at(L.y)), o.gate_indx, a->M, a->top_k, a->K,

@@ -46,6 +46,17 @@ struct GemmParams {
   // (expert, N-tile, first row, end row), filled by a small kernel before the
   // GEMM (replaces the dependent routing loads of every workgroup's prologue)
   int4* tile_lut;
+  // prefill GEMM2 tail split (0 = off): each XCD's logical tiles run whole
+  // (bf16 rows, y_bf16) except the last partial round's, which are split up
+  // to tail_split ways along the reduction dim so they fill one round of the
+  // XCD's tail_slots workgroup slots; their fp32 partials go to tail_part
+  // ([pair][BM][BN], pairs numbered XCD by XCD, tile * S + split within one) and
+  // tail_fold_kernel adds them into the bf16 rows
+  int tail_split;
+  int tail_slots;
+  float* tail_part;
+  int64_t tail_pairs;  // capacity of tail_part in [BM][BN] partials (set by the launcher)
+  size_t tail_bytes;   // size of tail_part
   // epilogue (fmoe_epilogue): activation, fp32 bias [E, Nout], swiglu alpha / limit
   int act;
   const float* bias;
@@ -62,6 +73,7 @@ enum Act { kActSilu = 0, kActGelu = 1, kActSwiglu = 2 };
 
 enum class Mode { kGemm1Silu, kGemm2 };
 enum class WType { kBf16, kFp8, kInt4, kMxfp4 };
+constexpr int kTailMaxSplit = 4;  // prefill GEMM2 tail split: ways per tail tile
 
 // Weight row of GEMM1 output column c: gate (u = 0) or up / linear (u = 1).
 // SiLU and GELU use split halves (gate c, up N + c), SWIGLU interleaved rows

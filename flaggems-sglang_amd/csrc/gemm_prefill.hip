@@ -34,6 +34,8 @@
 // lanes; silu(gate) * up is formed in registers and only the bf16 activation
 // is written.  GEMM2: rows scaled by the routing weight, fp32 partial per
 // slot; the top-k sum runs in fmoe_moe_sum (fixed order, deterministic).
+#include <algorithm>
+
 #include "gemm.hpp"
 
 namespace fmoe {
@@ -203,6 +205,39 @@ __device__ __forceinline__ Tile tile_of(const GemmParams& p, int L, int lane) {
   return t;
 }
 
+// Tail split of XCD x (GEMM2, p.tail_split > 1): the XCD's logical tiles are
+// [base, base + Tx) (xcd_remap's partition of the T live tiles).  Whole
+// tiles fill rounds of `slots` workgroups; the tl = Tx % slots tiles of the
+// last partial round are split S = min(max_split, slots / tl, stages) ways,
+// so their tl * S workgroups fill at most one round.  S = 1: no split, every
+// tile whole.  The GEMM and tail_fold_kernel derive the same plan.
+struct TailPlan {
+  int base, full, tl, S;
+};
+__device__ __forceinline__ TailPlan tail_plan(int T, int x, int max_split, int slots, int stages) {
+  const int q = T / kNumXcd, r8 = T % kNumXcd;
+  const int Tx = q + (x < r8 ? 1 : 0);
+  TailPlan t;
+  t.base = x * q + min(x, r8);
+  t.tl = Tx % slots;
+  t.S = t.tl > 0 ? min(min(max_split, slots / t.tl), stages) : 1;
+  if (t.S < 2) {
+    t.S = 1;
+    t.tl = 0;
+  }
+  t.full = Tx - t.tl;
+  return t;
+}
+// Index of XCD x's first tail pair: the pairs of XCDs 0 .. x-1 come first.
+__device__ __forceinline__ int tail_offset(int T, int x, int max_split, int slots, int stages) {
+  int off = 0;
+  for (int y = 0; y < x; ++y) {
+    const TailPlan t = tail_plan(T, y, max_split, slots, stages);
+    off += t.tl * t.S;
+  }
+  return off;
+}
+
 // Fills p.tile_lut for every live logical tile: one wave per tile.
 template <int BM>
 __global__ __launch_bounds__(256) void tile_lut_kernel(GemmParams p) {
@@ -211,6 +246,70 @@ __global__ __launch_bounds__(256) void tile_lut_kernel(GemmParams p) {
   if (L >= *p.n_tiles * p.n_ntiles) return;
   const Tile t = tile_of<BM>(p, L, lane);
   if (lane == 0) p.tile_lut[L] = int4{t.e, t.nt, t.row_beg, t.row_end};
+}
+
+// Adds the tail-split partials of each split tile in split order and writes
+// the tile's bf16 rows (y_bf16 layout [slot][Nout]): one workgroup per (XCD,
+// tail tile, 16-row chunk), every partial of the chunk loaded before the
+// adds.  Bias and routing weight are already in the partials.
+constexpr int kFoldRows = 16;
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void tail_fold_kernel(GemmParams p, int stages) {
+  constexpr int kChunks = BM / kFoldRows;
+  constexpr int kVec = kFoldRows * BN / (4 * 256);  // float4 per thread and partial
+  static_assert(kFoldRows * BN % (4 * 256) == 0, "fold chunk");
+  const int rc = blockIdx.x % kChunks;
+  const int xt = blockIdx.x / kChunks;
+  const int x = xt / p.tail_slots, t = xt % p.tail_slots;
+  const int T = *p.n_tiles * p.n_ntiles;
+  const TailPlan pl = tail_plan(T, x, p.tail_split, p.tail_slots, stages);
+  if (t >= pl.tl) return;
+  const int pair0 = tail_offset(T, x, p.tail_split, p.tail_slots, stages) + t * pl.S;
+  if (pair0 + pl.S > p.tail_pairs) return;
+  const int L = pl.base + pl.full + t;
+  int nt, rb, re;
+  if (p.tile_lut) {
+    const int4 v = p.tile_lut[L];
+    nt = v.y;
+    rb = v.z;
+    re = v.w;
+  } else {
+    const Tile tt = tile_of<BM>(p, L, threadIdx.x % kWave);
+    nt = tt.nt;
+    rb = tt.row_beg;
+    re = tt.row_end;
+  }
+  const int r0 = rc * kFoldRows;
+  if (r0 >= re - rb) return;
+  const int64_t c0 = static_cast<int64_t>(nt) * BN;
+  const int cols = static_cast<int>(min(static_cast<int64_t>(BN), p.Nout - c0));
+  const float* part = p.tail_part + static_cast<int64_t>(pair0) * (BM * BN) + r0 * BN;
+  float4 a[kVec];
+#pragma unroll
+  for (int v = 0; v < kVec; ++v) a[v] = *reinterpret_cast<const float4*>(part + (threadIdx.x + v * 256) * 4);
+  for (int sp = 1; sp < pl.S; ++sp) {
+    float4 b[kVec];
+#pragma unroll
+    for (int v = 0; v < kVec; ++v)
+      b[v] = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(sp) * (BM * BN) + (threadIdx.x + v * 256) * 4);
+#pragma unroll
+    for (int v = 0; v < kVec; ++v) {
+      a[v].x += b[v].x;
+      a[v].y += b[v].y;
+      a[v].z += b[v].z;
+      a[v].w += b[v].w;
+    }
+  }
+  uint16_t* y = static_cast<uint16_t*>(p.out);
+#pragma unroll
+  for (int v = 0; v < kVec; ++v) {
+    const int idx = (threadIdx.x + v * 256) * 4;
+    const int r = idx / BN, c = idx - (idx / BN) * BN;
+    if (r0 + r >= re - rb || c >= cols) continue;
+    const uint32_t w0 = f32_to_bf16(a[v].x) | (static_cast<uint32_t>(f32_to_bf16(a[v].y)) << 16);
+    const uint32_t w1 = f32_to_bf16(a[v].z) | (static_cast<uint32_t>(f32_to_bf16(a[v].w)) << 16);
+    *reinterpret_cast<uint2*>(y + static_cast<int64_t>(rb + r0 + r) * p.Nout + c0 + c) = make_uint2(w0, w1);
+  }
 }
 
 template <class C, int ACT>
@@ -231,11 +330,35 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   // XCD-contiguous, then mapped by tile_of (or its precomputed table).
   const int nn = p.n_ntiles;
   const int per_split = *p.n_tiles * nn;
-  const int live = per_split * p.splits;
-  if (static_cast<int>(blockIdx.x) >= live) return;
-  int L = xcd_remap(blockIdx.x, live);
-  const int split = L / per_split;
-  L -= split * per_split;
+  const int64_t kbytes = FP8 ? p.Kred : p.Kred * 2;  // bytes per operand row
+  const int nk_all = static_cast<int>(kbytes / SB);
+  int L, split, n_splits = p.splits;
+  int tail = -1;  // tail-split workgroup: its pair index in p.tail_part
+  if (MODE == Mode::kGemm2 && p.tail_split > 1) {
+    const TailPlan t = tail_plan(per_split, static_cast<int>(blockIdx.x) % kNumXcd, p.tail_split,
+                                 p.tail_slots, nk_all);
+    const int i = static_cast<int>(blockIdx.x) / kNumXcd;  // dispatch position within the XCD
+    if (i < t.full) {
+      L = t.base + i;
+      split = 0;
+      n_splits = 1;
+    } else {
+      const int j = i - t.full;
+      if (j >= t.tl * t.S) return;
+      L = t.base + t.full + j / t.S;
+      split = j % t.S;
+      n_splits = t.S;
+      tail = tail_offset(per_split, static_cast<int>(blockIdx.x) % kNumXcd, p.tail_split, p.tail_slots,
+                         nk_all) + j;
+      if (tail >= p.tail_pairs) return;  // the host sizes tail_part for every pair
+    }
+  } else {
+    const int live = per_split * p.splits;
+    if (static_cast<int>(blockIdx.x) >= live) return;
+    L = xcd_remap(blockIdx.x, live);
+    split = L / per_split;
+    L -= split * per_split;
+  }
   int e, nt, row_beg, row_end;
   if (p.tile_lut) {
     const int4 v = p.tile_lut[L];
@@ -259,11 +382,9 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   const bool wave_live = C::WAVES_M == 1 || MODE == Mode::kGemm1Silu ||
                          __builtin_amdgcn_readfirstlane(row_end - row_beg > wm * WM);
 
-  const int64_t kbytes = FP8 ? p.Kred : p.Kred * 2;  // bytes per operand row
-  const int nk_all = static_cast<int>(kbytes / SB);
   const int ksb = static_cast<int>(p.Kred / 128);      // fp8 scale blocks per row
   // split-K: this workgroup reduces stages [k0, k0 + nk)
-  const int per_k = (nk_all + p.splits - 1) / p.splits;
+  const int per_k = (nk_all + n_splits - 1) / n_splits;
   const int k0 = min(nk_all, split * per_k);
   const int nk = min(nk_all, k0 + per_k) - k0;
 
@@ -561,6 +682,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       return;
     }
   }
+  const bool y_rows_bf16 = p.y_bf16 && tail < 0;  // whole tile, one split: bf16 slot rows
 #pragma unroll
   for (int i = 0; i < MI; ++i) {
     const int s = row_beg + wm * WM + i * 16 + orow;
@@ -589,8 +711,12 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
         if (ok && col < p.N_act) *reinterpret_cast<uint2*>(act + col) = make_uint2(w[0], w[1]);
       }
     } else {
-      float* y = static_cast<float*>(p.out) + split * p.out_split_stride +
-                 static_cast<int64_t>(s) * p.Nout;
+      // fp32 destination row: a split plane's slot row, or the tile's row of
+      // its tail-split partial ([BM][BN] within the tile)
+      float* y = tail >= 0 ? p.tail_part + static_cast<int64_t>(tail) * (BM * BN) +
+                                 (wm * WM + i * 16 + orow) * BN - static_cast<int64_t>(nt) * BN
+                           : static_cast<float*>(p.out) + split * p.out_split_stride +
+                                 static_cast<int64_t>(s) * p.Nout;
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
         f32x4_t v = acc[i][j];
@@ -601,7 +727,7 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
           for (int c = 0; c < 4; ++c) v[c] += bv[j][c];
         }
         if (ok && col < p.Nout) {
-          if (p.y_bf16) {
+          if (y_rows_bf16) {
             // one split: the row goes out as bf16, like SGLang's per-slot
             // intermediate before its top-k sum
             uint16_t* yb = static_cast<uint16_t*>(p.out) + static_cast<int64_t>(s) * p.Nout + col;
@@ -617,6 +743,31 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
   }
 }
 
+// Workgroup slots of one XCD for a configuration's kernel (workgroups per CU
+// x CUs per XCD); 0 when the runtime cannot say (the tail split is then off).
+template <class C>
+int xcd_slots() {
+  static const int slots = [] {
+    int dev = 0, cus = 0, occ = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemm_prefill_kernel<C, kActSilu>, C::NT, 0) != hipSuccess)
+      return 0;
+    return (cus % kNumXcd == 0 && occ > 0) ? occ * (cus / kNumXcd) : 0;
+  }();
+  return slots;
+}
+
+// Partials the tail split of a GEMM2 launch may need: at most one round of
+// an XCD's slots per XCD, and at most kTailMaxSplit per live tile.
+template <class C>
+int64_t tail_pairs_for(int64_t max_tiles, int64_t Nout) {
+  const int slots = xcd_slots<C>();
+  if (slots <= 0) return 0;
+  const int64_t nn = (Nout + C::BN - 1) / C::BN;
+  return std::min<int64_t>(static_cast<int64_t>(kNumXcd) * slots, max_tiles * nn * kTailMaxSplit);
+}
+
 template <class C>
 int launch(const GemmParams& p0, hipStream_t s) {
   GemmParams p = p0;
@@ -625,7 +776,19 @@ int launch(const GemmParams& p0, hipStream_t s) {
   p.n_ntiles = static_cast<int>((ncols + per_tile - 1) / per_tile);
   if (p.group_tiles <= 0) p.group_tiles = kGroupTiles;
   if (p.splits < 1) p.splits = 1;
-  const int64_t grid = static_cast<int64_t>(p.max_tiles) * p.n_ntiles * p.splits;
+  int64_t grid = static_cast<int64_t>(p.max_tiles) * p.n_ntiles * p.splits;
+  if (C::MODE == Mode::kGemm2 && p.tail_split > 1) {
+    const int slots = xcd_slots<C>();
+    const int64_t pairs = tail_pairs_for<C>(p.max_tiles, p.Nout);
+    p.tail_pairs = static_cast<int64_t>(p.tail_bytes / (static_cast<size_t>(C::BM) * C::BN * sizeof(float)));
+    if (slots <= 0 || !p.tail_part || pairs <= 0 || p.tail_pairs < pairs || p.splits != 1 || !p.y_bf16) {
+      p.tail_split = 0;  // whole tiles only
+    } else {
+      p.tail_slots = slots;
+      const int64_t per_xcd = (static_cast<int64_t>(p.max_tiles) * p.n_ntiles + kNumXcd - 1) / kNumXcd;
+      grid = kNumXcd * (per_xcd + slots);  // whole tiles + one round of tail workgroups per XCD
+    }
+  }
   if (grid <= 0) return FMOE_OK;
   if (grid > 0x7fffffff) return fmoe_host::fail(FMOE_ERR_UNSUPPORTED, "prefill grid too large");
   if (C::FP8 && p.Kred / 128 > C::KST)
@@ -642,6 +805,11 @@ int launch(const GemmParams& p0, hipStream_t s) {
     gemm_prefill_kernel<C, kActGelu><<<g, b, 0, s>>>(p);
   else
     gemm_prefill_kernel<C, kActSwiglu><<<g, b, 0, s>>>(p);
+  if (C::MODE == Mode::kGemm2 && p.tail_split > 1) {
+    const int stages = static_cast<int>((C::FP8 ? p.Kred : 2 * p.Kred) / C::SB);
+    tail_fold_kernel<C::BM, C::BN>
+        <<<dim3(static_cast<unsigned>(kNumXcd * p.tail_slots * (C::BM / kFoldRows))), dim3(256), 0, s>>>(p, stages);
+  }
   return fmoe_host::check_launch("gemm_prefill");
 }
 
@@ -679,6 +847,27 @@ int launch_prefill(WType wt, Mode mode, int bm, const GemmParams& p, hipStream_t
 #undef L
   return fmoe_host::fail(FMOE_ERR_UNSUPPORTED,
                          "prefill: block_m=%d is not supported for this weight type", bm);
+}
+
+// Bytes of the tail-split partial buffer for a fused prefill GEMM2 of this
+// weight type and tile height (the configuration launch_prefill picks).
+size_t prefill_tail_bytes(WType wt, int bm, int64_t max_tiles, int64_t Nout) {
+  using namespace prefill;
+#define T(BM, BN, WMS, WNS, SB, NB, F8) \
+  static_cast<size_t>(tail_pairs_for<Cfg<BM, BN, WMS, WNS, SB, NB, F8, Mode::kGemm2>>(max_tiles, Nout)) * BM * BN * 4
+  if (wt != WType::kFp8) {
+    if (wt != WType::kBf16) return 0;
+    if (bm == 256) return T(256, 256, 4, 2, 128, 2, false);
+    if (bm == 160) return T(160, 256, 2, 4, 128, 3, false);
+    if (bm == 128) return T(128, 256, 2, 4, 128, 3, false);
+    if (bm == 64) return T(64, 256, 1, 4, 64, 4, false);
+  } else {
+    if (bm == 160) return T(160, 384, 2, 4, 128, 2, true);
+    if (bm == 128) return T(128, 256, 2, 4, 128, 3, true);
+    if (bm == 64) return T(64, 256, 1, 8, 128, 3, true);
+  }
+#undef T
+  return 0;
 }
 
 }  // namespace fmoe

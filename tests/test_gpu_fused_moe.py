@@ -266,8 +266,11 @@ def test_product_quantizers_match_oracle():
 # --------------------------------------------- full-size, size-independent checks
 def test_mixtral_prefill_permutation_and_determinism():
     """Mixtral bf16 at M=4096 (the bench workload): outputs are bit-identical
-    across runs, and permuting the tokens permutes the output rows exactly
-    (each row's arithmetic does not depend on its neighbours)."""
+    across runs, and permuting the tokens permutes the output rows -- exactly
+    except for rows that land in a GEMM2 tail-split tile in one of the two
+    runs (each XCD's last partial round of tiles is reduced in split parts,
+    and which tiles those are follows the token order), which agree to bf16
+    rounding.  The whole output against the oracle."""
     M, K, N, E, k = 4096, 4096, 14336, 8, 2
     gen = torch.Generator(device=DEV).manual_seed(7)
     x = torch.randn(M, K, device=DEV, generator=gen).to(torch.bfloat16)
@@ -280,15 +283,15 @@ def test_mixtral_prefill_permutation_and_determinism():
     assert torch.equal(a, b)
     perm = torch.randperm(M, device=DEV, generator=gen)
     c = flaggems_sglang.fused_experts(x[perm], w13, w2, tw[perm], ti[perm])
-    assert torch.equal(c, a[perm])
-    # spot-check 8 tokens against the oracle
-    sel = perm[:8].cpu()
-    xs, ws, ids = x[sel.to(DEV)].cpu(), tw[sel.to(DEV)].cpu(), ti[sel.to(DEV)].cpu()
-    used = sorted(set(ids.flatten().tolist()))
-    remap = {e: i for i, e in enumerate(used)}
-    ids_l = ids.clone().apply_(lambda e: remap[e])
-    ref = O.fused_experts(xs, w13[used].cpu(), w2[used].cpu(), ws, ids_l)
-    _close(a[sel.to(DEV)], ref, 2e-2)
+    differ = (c != a[perm]).any(dim=1).float().mean().item()
+    assert differ < 0.5, f"{differ:.2%} of the rows differ under the permutation"
+    # a slot row's bf16 rounding can flip by one ulp, and the top-k sum can
+    # cancel it to a small output: the absolute part scales with the RMS
+    rms = float(a.float().pow(2).mean().sqrt())
+    torch.testing.assert_close(c.float(), a[perm].float(), rtol=2 ** -7, atol=2 ** -7 * rms)
+    ref = O.fused_experts(x.cpu(), w13.cpu(), w2.cpu(), tw.cpu(), ti.cpu())
+    _close(a, ref, 2e-2)
+    _close_literal(a, ref, 2e-2)
 
 
 # ------------------------------------------------------------ activations / bias path
@@ -399,10 +402,12 @@ def test_tiny_decode_path_equals_aligned_path(M, fp8):
 def test_fp8_fused_act_quant_matches_stage_path(M, on_input):
     """The fused fp8 prefill path quantizes the GEMM1 activation in the GEMM1
     epilogue; the stage path (triton_kernel_fused_experts) runs the separate
-    fmoe_quant_fp8_group pass on the bf16 activation.  With N large enough
-    that GEMM2 splits K (fp32 partial planes in both paths; a split needs >= 64
-    stages of 128 on each side, so N >= 16384) the two must agree bit for
-    bit."""
+    fmoe_quant_fp8_group pass on the bf16 activation.  At N = 16384 the
+    stage path splits GEMM2 into fp32 planes while the fused path keeps whole
+    tiles as bf16 slot rows and splits only each XCD's tail tiles, so the two
+    differ by GEMM2 summation order and the slot rows' bf16 rounding (about
+    one bf16 ulp of an output): far inside the fp8 tolerance, and a wrong
+    activation code would be a much larger error only where it matters."""
     K, N, E, k = 512, 16384, 8, 2
     d = O.make_inputs(M, K, N, E, k, wscale=0.02)
     q1, s1 = Q.quantize_fp8_block(d["w13"].to(DEV))
@@ -416,7 +421,11 @@ def test_fp8_fused_act_quant_matches_stage_path(M, on_input):
         x, q1.transpose(1, 2), q2.transpose(1, 2), rd, gi, si, use_fp8_w8a8=True,
         w1_scale=s1.transpose(1, 2), w2_scale=s2.transpose(1, 2), block_shape=[128, 128],
         apply_router_weight_on_input=on_input)
-    assert torch.equal(fused, staged)
+    f, g = fused.float(), staged.float()
+    rms = float(g.pow(2).mean().sqrt())
+    torch.testing.assert_close(f, g, rtol=2 ** -6, atol=2 ** -6 * rms)
+    rel = float((f - g).norm() / g.norm())
+    assert rel < 4e-3, f"relative difference {rel:.3e}"
 
 
 @pytest.mark.parametrize("M", [1, 5, 16])
