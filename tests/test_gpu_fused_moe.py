@@ -428,6 +428,34 @@ def test_fp8_fused_act_quant_matches_stage_path(M, on_input):
     assert rel < 4e-3, f"relative difference {rel:.3e}"
 
 
+@pytest.mark.parametrize("on_input", [False, True])
+def test_fp8_fused_act_quant_bit_exact_identity_w2(on_input):
+    """Pins the fused fp8 path's in-epilogue activation quantization bit for
+    bit against the stage path's separate fmoe_quant_fp8_group pass.  With
+    K = N, w2 = the identity (fp8, 128x128 block scales) and top-1 routing,
+    each GEMM2 output element has exactly one nonzero term, so every GEMM2
+    summation order (whole tiles, tail split, split-K planes) gives the same
+    bits, and the two outputs can differ only through the activation codes
+    and scales."""
+    M, K, E, k = 512, 512, 4, 1
+    N = K
+    d = O.make_inputs(M, K, N, E, k, wscale=0.02)
+    eye = torch.eye(K, dtype=torch.bfloat16).expand(E, K, K).contiguous()
+    q1, s1 = Q.quantize_fp8_block(d["w13"].to(DEV))
+    q2, s2 = Q.quantize_fp8_block(eye.to(DEV))
+    tw, ti = d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    x = d["x"].to(DEV)
+    fused = flaggems_sglang.fused_experts(x, q1, q2, tw, ti, use_fp8_w8a8=True, w1_scale=s1, w2_scale=s2,
+                                          block_shape=[128, 128], apply_router_weight_on_input=on_input)
+    rd, gi, si = F._standard_topk_to_triton_kernels(tw, ti, E)
+    staged = flaggems_sglang.triton_kernel_fused_experts(
+        x, q1.transpose(1, 2), q2.transpose(1, 2), rd, gi, si, use_fp8_w8a8=True,
+        w1_scale=s1.transpose(1, 2), w2_scale=s2.transpose(1, 2), block_shape=[128, 128],
+        apply_router_weight_on_input=on_input)
+    assert torch.count_nonzero(fused) > fused.numel() // 2  # a real activation, not zeros
+    assert torch.equal(fused, staged)
+
+
 @pytest.mark.parametrize("M", [1, 5, 16])
 def test_int4_identity_expert_map_bit_exact(M):
     """int4 decode with an identity expert map (the expert-parallel routing
