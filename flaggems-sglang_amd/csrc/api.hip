@@ -617,7 +617,6 @@ extern "C" int fmoe_fused_experts(const fmoe_fused_args* a, void* stream) {
                 L.total);
   char* ws = static_cast<char*>(a->workspace);
   auto at = [&](size_t o) { return static_cast<void*>(ws + o); };
-  const int64_t slots = a->M * a->top_k;
   if (tiny_decode(a, L)) return fused_tiny(a, L, ws, static_cast<hipStream_t>(stream));
 
   fmoe_align_out o{};
