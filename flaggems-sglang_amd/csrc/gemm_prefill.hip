@@ -32,8 +32,11 @@
 // GEMM1 (gate/up + SiLU): each wave's BN/WAVES_N weight rows are half gate rows
 // and the matching up rows, so gate block j and up block j sit in the same
 // lanes; silu(gate) * up is formed in registers and only the bf16 activation
-// is written.  GEMM2: rows scaled by the routing weight, fp32 partial per
-// slot; the top-k sum runs in fmoe_moe_sum (fixed order, deterministic).
+// is written.  GEMM2: rows scaled by the routing weight; each slot row is
+// stored as bf16 (one split), as fp32 split-K planes (stage-level calls), or,
+// for the tail tiles of the fused path's tail split, as fp32 parts that
+// tail_fold_kernel adds; the top-k sum runs in its own fixed-order launch
+// (deterministic).
 #include <algorithm>
 
 #include "gemm.hpp"
