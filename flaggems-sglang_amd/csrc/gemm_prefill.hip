@@ -715,7 +715,9 @@ __global__ __launch_bounds__(C::NT) void gemm_prefill_kernel(GemmParams p) {
       }
     } else {
       // fp32 destination row: a split plane's slot row, or the tile's row of
-      // its tail-split partial ([BM][BN] within the tile)
+      // its tail-split partial ([BM][BN] within the tile; the row pointer is
+      // taken back by the tile's first column, which `col` adds again, so
+      // both cases share one store)
       float* y = tail >= 0 ? p.tail_part + static_cast<int64_t>(tail) * (BM * BN) +
                                  (wm * WM + i * 16 + orow) * BN - static_cast<int64_t>(nt) * BN
                            : static_cast<float*>(p.out) + split * p.out_split_stride +
