@@ -5,7 +5,7 @@ a long reduction) run whole tiles as bf16 slot rows and split only each XCD's
 last partial round; ``tail_fold_kernel`` adds the parts.  These shapes take
 that route (asserted through the C ABI's own split rule), with K = 640 so the
 last output tile is partial (640 = 2 x 256 + 128), across the bf16 tile
-heights 64 / 160 / 256 and the fp8 128-row tiles.  Whole output against the
+heights 64 / 160 / 256, the fp8 128-row tiles and SwiGLU with both biases.  Whole output against the
 oracle, and bit identity across runs.
 """
 
@@ -65,3 +65,42 @@ def test_fp8_tail_split():
     assert torch.equal(a, b)
     ref = O.fused_experts_fp8(d["x"], q1.cpu(), s1.cpu(), q2.cpu(), s2.cpu(), d["topk_weights"], d["topk_ids"])
     _close(a, ref, 5e-2)
+
+
+@pytest.mark.parametrize("M", [64, 256])
+def test_bf16_swiglu_bias_tail_split(M):
+    """SwiGLU with both biases (alpha, clamp) through the C ABI's fused path at
+    tail-split shapes: GEMM2's bias enters the split-0 part only, so every
+    output adds it once.  Against the bias path's oracle."""
+    K, N, E, k = 640, 8192, 4, 2
+    got_bm, tail = _takes_tail_split(_lib.W_BF16, M, K, N, E, k)
+    assert got_bm > 16 and tail
+    d = O.make_inputs(M, K, N, E, k, wscale=0.02)
+    g = torch.Generator().manual_seed(M)
+    b13 = torch.randn(E, 2 * N, generator=g) * 0.1
+    b2 = torch.randn(E, K, generator=g) * 0.1
+    alpha, limit = 1.702, 7.0
+    x, tw, ti = d["x"].to(DEV), d["topk_weights"].to(DEV), d["topk_ids"].to(DEV)
+    w13, w2 = d["w13"].to(DEV), d["w2"].to(DEV)
+    b13d, b2d = b13.to(DEV), b2.to(DEV)
+    L = _lib.lib()
+    st = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        out = torch.empty(M, K, dtype=torch.bfloat16, device=DEV)
+        a = _lib.FusedArgs(_lib.W_BF16, x.data_ptr(), M, K, N, E, k, w13.data_ptr(), w2.data_ptr(),
+                           None, None, None, None, 128, tw.data_ptr(), ti.data_ptr(), 0, 1.0, 0,
+                           out.data_ptr(), None, 0, _lib.ACT_SWIGLU, b13d.data_ptr(), b2d.data_ptr(),
+                           alpha, limit, None, 0)
+        n = L.fmoe_fused_experts_workspace_bytes(ctypes.byref(a))
+        ws = torch.empty(max(n, 1), dtype=torch.uint8, device=DEV)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), n
+        _lib.check(L.fmoe_fused_experts(ctypes.byref(a), st), "fused_experts")
+        torch.cuda.synchronize()
+        return out
+
+    a = run()
+    assert torch.equal(a, run())
+    ref = O.fused_experts_bias(d["x"], d["w13"], b13, d["w2"], b2, d["topk_weights"], d["topk_ids"],
+                               alpha=alpha, limit=limit)
+    _close(a, ref, 2e-2)
