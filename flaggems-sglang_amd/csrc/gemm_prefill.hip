@@ -756,8 +756,10 @@ int xcd_slots() {
     int dev = 0, cus = 0, occ = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemm_prefill_kernel<C, kActSilu>, C::NT, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, gemm_prefill_kernel<C, kActSilu>, C::NT, 0) != hipSuccess) {
+      (void)hipGetLastError();  // not left for the next launch's check to report
       return 0;
+    }
     return (cus % kNumXcd == 0 && occ > 0) ? occ * (cus / kNumXcd) : 0;
   }();
   return slots;
