@@ -77,6 +77,16 @@ def test_noalloc_bf16_matches(Ms):
         assert torch.equal(out, ref)
 
 
+def test_noalloc_tail_split_matches():
+    """Prefill GEMM2 with the tail split (few output tiles, a long reduction):
+    the split parts and their fold live in the shared array too; a larger
+    then a smaller call, each equal to the allocating path."""
+    for M in (256, 64):
+        x, w13, w2, tw, ti = _inputs(M, 640, 8192, 4, 2)
+        out, ref = _both(_lib.W_BF16, x, w13, w2, tw, ti)
+        assert torch.equal(out, ref)
+
+
 def test_noalloc_fp8_and_int4_match():
     for M in (200, 5):
         x, w13, w2, tw, ti = _inputs(M, 512, 256, 8, 2)
